@@ -1,0 +1,338 @@
+// C ABI of libflock_attn.so: argument checks, error reporting, streams,
+// memory helpers and the entry points declared in include/flock_attn.h.
+//
+// Every entry point validates its arguments on the host before touching the
+// device, so a rejected call has no side effect -- the reference's Layer
+// throws before encoding anything (kernels/layer.ts:575, 689-698; lib.ts:504-506).
+#include <stdarg.h>
+#include <stdio.h>
+#include <string.h>
+
+#include "common.hpp"
+
+namespace flk {
+
+static thread_local char g_err[512] = "";
+static hipStream_t g_stream = nullptr;
+
+hipStream_t Stream::get() { return g_stream; }
+
+static int32_t fail(int32_t code, const char* fmt, ...) {
+  va_list ap;
+  va_start(ap, fmt);
+  vsnprintf(g_err, sizeof(g_err), fmt, ap);
+  va_end(ap);
+  return code;
+}
+
+static int32_t hip_status(hipError_t e, const char* what) {
+  if (e == hipSuccess) return FLK_OK;
+  return fail(FLK_ERR_HIP, "%s: %s", what, hipGetErrorString(e));
+}
+
+static int32_t check_heads(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim) {
+  if (n_heads == 0 || n_kv_heads == 0)
+    return fail(FLK_ERR_ARG, "n_heads (%u) and n_kv_heads (%u) must be >= 1", n_heads, n_kv_heads);
+  if (n_heads % n_kv_heads != 0)
+    return fail(FLK_ERR_ARG, "n_heads %u is not a multiple of n_kv_heads %u", n_heads, n_kv_heads);
+  if (n_heads / n_kv_heads > 8)
+    return fail(FLK_ERR_UNSUPPORTED, "GQA group %u > 8 is not supported", n_heads / n_kv_heads);
+  if (head_dim != 64 && head_dim != 128)
+    return fail(FLK_ERR_UNSUPPORTED, "head_dim %u not supported (64 or 128)", head_dim);
+  return FLK_OK;
+}
+
+static int32_t check_ws(void* ws, uint64_t ws_bytes, uint64_t need) {
+  if (ws == nullptr || ws_bytes < need)
+    return fail(FLK_ERR_WORKSPACE, "workspace of %llu bytes needed, got %llu%s",
+                (unsigned long long)need, (unsigned long long)ws_bytes,
+                ws == nullptr ? " (null)" : "");
+  if (reinterpret_cast<uintptr_t>(ws) % 256 != 0)
+    return fail(FLK_ERR_WORKSPACE, "workspace must be 256-byte aligned");
+  return FLK_OK;
+}
+
+#define FLK_NONNULL(p)                                                  \
+  do {                                                                  \
+    if ((p) == nullptr) return fail(FLK_ERR_ARG, "%s is null", #p);     \
+  } while (0)
+
+}  // namespace flk
+
+using namespace flk;
+
+extern "C" {
+
+const char* flk_last_error(void) { return g_err; }
+
+const char* flk_version(void) { return "flock_attn 0.1 (gfx950)"; }
+
+int32_t flk_device_count(int32_t* count) {
+  FLK_NONNULL(count);
+  int n = 0;
+  if (hipGetDeviceCount(&n) != hipSuccess) n = 0;
+  *count = n;
+  return FLK_OK;
+}
+
+int32_t flk_set_stream(void* stream) {
+  g_stream = static_cast<hipStream_t>(stream);
+  return FLK_OK;
+}
+
+int32_t flk_alloc(void** dptr, uint64_t bytes) {
+  FLK_NONNULL(dptr);
+  if (bytes == 0) return fail(FLK_ERR_ARG, "flk_alloc of 0 bytes");
+  return hip_status(hipMalloc(dptr, bytes), "hipMalloc");
+}
+
+int32_t flk_free(void* dptr) {
+  if (dptr == nullptr) return FLK_OK;
+  // Work still queued may read this buffer (a caller can drop its last
+  // reference right after a launch), so drain the device first.
+  hipError_t e = hipDeviceSynchronize();
+  if (e == hipSuccess) e = hipFree(dptr);
+  return hip_status(e, "hipFree");
+}
+
+int32_t flk_h2d(void* dst, const void* host_src, uint64_t bytes, uint64_t dst_off) {
+  FLK_NONNULL(dst);
+  FLK_NONNULL(host_src);
+  if (bytes == 0) return FLK_OK;
+  hipError_t e = hipMemcpyAsync(static_cast<char*>(dst) + dst_off, host_src, bytes,
+                                hipMemcpyHostToDevice, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  return hip_status(e, "flk_h2d");
+}
+
+int32_t flk_d2h(void* host_dst, const void* src, uint64_t bytes, uint64_t src_off) {
+  FLK_NONNULL(host_dst);
+  FLK_NONNULL(src);
+  if (bytes == 0) return FLK_OK;
+  hipError_t e = hipMemcpyAsync(host_dst, static_cast<const char*>(src) + src_off, bytes,
+                                hipMemcpyDeviceToHost, g_stream);
+  if (e == hipSuccess) e = hipStreamSynchronize(g_stream);
+  return hip_status(e, "flk_d2h");
+}
+
+int32_t flk_memset(void* dst, int32_t value, uint64_t bytes) {
+  FLK_NONNULL(dst);
+  if (bytes == 0) return FLK_OK;
+  return hip_status(hipMemsetAsync(dst, value, bytes, g_stream), "hipMemsetAsync");
+}
+
+int32_t flk_sync(void) { return hip_status(hipStreamSynchronize(g_stream), "flk_sync"); }
+
+uint64_t flk_workspace_bytes(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                             uint32_t max_keys, uint32_t max_queries, uint32_t max_seqs) {
+  if (n_heads == 0 || n_kv_heads == 0 || n_heads % n_kv_heads != 0 || head_dim == 0) return 0;
+  if (max_keys == 0) max_keys = 1;
+  if (max_seqs == 0) max_seqs = 1;
+  const DecodeShape ds{n_heads, n_kv_heads, head_dim, max_seqs, max_keys};
+  uint64_t need = decode_ws_bound(ds);
+  // A single-sequence decode plans its splits on its own, so cover it too.
+  const DecodeShape ds1{n_heads, n_kv_heads, head_dim, 1, max_keys};
+  const uint64_t d1 = decode_ws_bound(ds1);
+  if (d1 > need) need = d1;
+  if (max_queries > 0) {
+    const uint32_t nq = max_queries < max_keys ? max_queries : max_keys;
+    const uint64_t b = prefill_ws_bound(n_heads, n_kv_heads, head_dim, nq, max_keys);
+    if (b > need) need = b;
+  }
+  return (need + 255) / 256 * 256;
+}
+
+uint64_t flk_call_workspace_bytes(int32_t kind, uint32_t n_heads, uint32_t n_kv_heads,
+                                  uint32_t head_dim, uint32_t n, uint32_t pos0, uint32_t n_seqs) {
+  if (n_heads == 0 || n_kv_heads == 0 || n_heads % n_kv_heads != 0 || head_dim == 0 || n == 0)
+    return 0;
+  switch (kind) {
+    case FLK_CALL_DECODE:
+      return decode_ws_bytes(DecodeShape{n_heads, n_kv_heads, head_dim, 1, n});
+    case FLK_CALL_RAGGED:
+      return decode_ws_bytes(DecodeShape{n_heads, n_kv_heads, head_dim, n_seqs ? n_seqs : 1, n});
+    case FLK_CALL_PREFILL:
+      return prefill_ws_bytes(prefill_plan(n_heads, n_kv_heads, head_dim, n, pos0), head_dim);
+    default:
+      return 0;
+  }
+}
+
+int32_t flk_workspace_init(void* ws, uint64_t ws_bytes) {
+  FLK_NONNULL(ws);
+  if (ws_bytes < kCounterBytes) return fail(FLK_ERR_WORKSPACE, "workspace smaller than counters");
+  return hip_status(hipMemsetAsync(ws, 0, kCounterBytes, g_stream), "flk_workspace_init");
+}
+
+int32_t flk_rmsnorm(const float* x, const float* g, float* o, uint32_t n, uint32_t n_vecs,
+                    float eps) {
+  FLK_NONNULL(x);
+  FLK_NONNULL(g);
+  FLK_NONNULL(o);
+  if (n == 0 || n_vecs == 0) return fail(FLK_ERR_ARG, "rmsnorm n=%u n_vecs=%u", n, n_vecs);
+  if (!(eps >= 0.f)) return fail(FLK_ERR_ARG, "rmsnorm eps must be >= 0");
+  return hip_status(launch_rmsnorm(x, g, o, n, n_vecs, eps, g_stream), "flk_rmsnorm");
+}
+
+int32_t flk_rope(float* x, const float* inv_freq, uint32_t n_tokens, uint32_t n_heads,
+                 uint32_t head_dim, uint32_t pos0, int32_t pairing) {
+  FLK_NONNULL(x);
+  FLK_NONNULL(inv_freq);
+  if (n_tokens == 0 || n_heads == 0 || head_dim == 0 || head_dim % 2 != 0)
+    return fail(FLK_ERR_ARG, "rope n_tokens=%u n_heads=%u head_dim=%u", n_tokens, n_heads,
+                head_dim);
+  if (pairing != FLK_ROPE_NEOX && pairing != FLK_ROPE_NORM)
+    return fail(FLK_ERR_ARG, "rope pairing %d (0 = neox, 1 = norm)", pairing);
+  return hip_status(launch_rope(x, inv_freq, n_tokens, n_heads, head_dim, pos0, pairing, g_stream),
+                    "flk_rope");
+}
+
+int32_t flk_kv_append(const float* kn, const float* v, float* kcache, float* vcache,
+                      uint32_t n_tokens, uint32_t pos0, uint32_t n_kv_heads, uint32_t head_dim,
+                      uint32_t max_keys) {
+  FLK_NONNULL(kn);
+  FLK_NONNULL(v);
+  FLK_NONNULL(kcache);
+  FLK_NONNULL(vcache);
+  if (n_tokens == 0 || n_kv_heads == 0 || head_dim == 0)
+    return fail(FLK_ERR_ARG, "kv_append n_tokens=%u n_kv_heads=%u head_dim=%u", n_tokens,
+                n_kv_heads, head_dim);
+  if ((uint64_t)pos0 + n_tokens > max_keys)
+    return fail(FLK_ERR_CACHE_FULL, "KV cache would exceed %u keys (%u + %u)", max_keys, pos0,
+                n_tokens);
+  return hip_status(
+      launch_kv_append(kn, v, kcache, vcache, n_tokens, pos0, n_kv_heads, head_dim, g_stream),
+      "flk_kv_append");
+}
+
+int32_t flk_qk_prologue(const float* q_raw, const float* k_raw, const float* v_raw,
+                        const float* gq, const float* gk, const float* inv_freq, float eps,
+                        int32_t pairing, float* qn_out, float* kcache, float* vcache,
+                        uint32_t n_tokens, uint32_t pos0, uint32_t n_heads, uint32_t n_kv_heads,
+                        uint32_t head_dim, uint32_t max_keys) {
+  FLK_NONNULL(q_raw);
+  FLK_NONNULL(k_raw);
+  FLK_NONNULL(v_raw);
+  FLK_NONNULL(gq);
+  FLK_NONNULL(gk);
+  FLK_NONNULL(inv_freq);
+  FLK_NONNULL(qn_out);
+  FLK_NONNULL(kcache);
+  FLK_NONNULL(vcache);
+  int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
+  if (rc) return rc;
+  if (n_tokens == 0) return fail(FLK_ERR_ARG, "n_tokens must be >= 1, got 0");
+  if (pairing != FLK_ROPE_NEOX && pairing != FLK_ROPE_NORM)
+    return fail(FLK_ERR_ARG, "rope pairing %d (0 = neox, 1 = norm)", pairing);
+  if ((uint64_t)pos0 + n_tokens > max_keys)
+    return fail(FLK_ERR_CACHE_FULL, "KV cache would exceed %u keys (%u + %u)", max_keys, pos0,
+                n_tokens);
+  return hip_status(launch_qk_prologue(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out,
+                                       kcache, vcache, n_tokens, pos0, n_heads, n_kv_heads,
+                                       head_dim, g_stream),
+                    "flk_qk_prologue");
+}
+
+int32_t flk_attn_decode(const float* q, const float* kcache, const float* vcache, float* o,
+                        uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim, uint32_t n_keys,
+                        void* ws, uint64_t ws_bytes) {
+  FLK_NONNULL(q);
+  FLK_NONNULL(kcache);
+  FLK_NONNULL(vcache);
+  FLK_NONNULL(o);
+  int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
+  if (rc) return rc;
+  if (n_keys == 0) return fail(FLK_ERR_ARG, "decode n_keys must be >= 1");
+  const DecodeShape s{n_heads, n_kv_heads, head_dim, 1, n_keys};
+  rc = check_ws(ws, ws_bytes, decode_ws_bytes(s));
+  if (rc) return rc;
+  return hip_status(launch_decode(q, kcache, vcache, o, nullptr, nullptr, s, nullptr, ws, g_stream),
+                    "flk_attn_decode");
+}
+
+int32_t flk_attn_prefill(const float* q, const float* kcache, const float* vcache, float* o,
+                         uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                         uint32_t n_queries, uint32_t pos0, void* ws, uint64_t ws_bytes) {
+  FLK_NONNULL(q);
+  FLK_NONNULL(kcache);
+  FLK_NONNULL(vcache);
+  FLK_NONNULL(o);
+  int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
+  if (rc) return rc;
+  if (n_queries == 0) return fail(FLK_ERR_ARG, "prefill n_queries must be >= 1");
+  if ((uint64_t)pos0 + n_queries > 0xFFFFFFFFull)
+    return fail(FLK_ERR_ARG, "pos0 + n_queries overflows");
+  const PrefillPlan p = prefill_plan(n_heads, n_kv_heads, head_dim, n_queries, pos0);
+  rc = check_ws(ws, ws_bytes, prefill_ws_bytes(p, head_dim));
+  if (rc) return rc;
+  return hip_status(launch_prefill(q, kcache, vcache, o, n_heads, n_kv_heads, head_dim, n_queries,
+                                   pos0, ws, g_stream),
+                    "flk_attn_prefill");
+}
+
+int32_t flk_decode_layer(const float* q_raw, const float* k_raw, const float* v_raw,
+                         const float* gq, const float* gk, const float* inv_freq, float eps,
+                         int32_t pairing, float* qn_out, float* kcache, float* vcache, float* o,
+                         uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                         uint32_t max_keys, void* ws, uint64_t ws_bytes) {
+  FLK_NONNULL(q_raw);
+  FLK_NONNULL(k_raw);
+  FLK_NONNULL(v_raw);
+  FLK_NONNULL(gq);
+  FLK_NONNULL(gk);
+  FLK_NONNULL(inv_freq);
+  FLK_NONNULL(qn_out);
+  FLK_NONNULL(kcache);
+  FLK_NONNULL(vcache);
+  FLK_NONNULL(o);
+  int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
+  if (rc) return rc;
+  if (pairing != FLK_ROPE_NEOX && pairing != FLK_ROPE_NORM)
+    return fail(FLK_ERR_ARG, "rope pairing %d (0 = neox, 1 = norm)", pairing);
+  if (pos >= max_keys) return fail(FLK_ERR_CACHE_FULL, "KV cache full at %u keys", max_keys);
+  const DecodeShape s{n_heads, n_kv_heads, head_dim, 1, pos + 1};
+  rc = check_ws(ws, ws_bytes, decode_ws_bytes(s));
+  if (rc) return rc;
+  DecodeFused f;
+  f.q_raw = q_raw;
+  f.k_raw = k_raw;
+  f.v_raw = v_raw;
+  f.gq = gq;
+  f.gk = gk;
+  f.inv_freq = inv_freq;
+  f.eps = eps;
+  f.pairing = pairing;
+  f.qn_out = qn_out;
+  f.kcache_w = kcache;
+  f.vcache_w = vcache;
+  return hip_status(launch_decode(qn_out, kcache, vcache, o, nullptr, nullptr, s, &f, ws, g_stream),
+                    "flk_decode_layer");
+}
+
+int32_t flk_attn_decode_ragged(const float* q, const float* kcache, const float* vcache,
+                               const uint64_t* seq_row_off, const uint32_t* n_keys, float* o,
+                               uint32_t n_seqs, uint32_t max_n_keys, uint32_t n_heads,
+                               uint32_t n_kv_heads, uint32_t head_dim, void* ws,
+                               uint64_t ws_bytes) {
+  FLK_NONNULL(q);
+  FLK_NONNULL(kcache);
+  FLK_NONNULL(vcache);
+  FLK_NONNULL(seq_row_off);
+  FLK_NONNULL(n_keys);
+  FLK_NONNULL(o);
+  int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
+  if (rc) return rc;
+  if (n_seqs == 0 || max_n_keys == 0)
+    return fail(FLK_ERR_ARG, "ragged decode n_seqs=%u max_n_keys=%u", n_seqs, max_n_keys);
+  if ((uint64_t)n_seqs * n_kv_heads > kMaxCounters)
+    return fail(FLK_ERR_UNSUPPORTED, "n_seqs * n_kv_heads exceeds %llu",
+                (unsigned long long)kMaxCounters);
+  const DecodeShape s{n_heads, n_kv_heads, head_dim, n_seqs, max_n_keys};
+  rc = check_ws(ws, ws_bytes, decode_ws_bytes(s));
+  if (rc) return rc;
+  return hip_status(
+      launch_decode(q, kcache, vcache, o, seq_row_off, n_keys, s, nullptr, ws, g_stream),
+      "flk_attn_decode_ragged");
+}
+
+}  // extern "C"

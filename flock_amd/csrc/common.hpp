@@ -1,0 +1,168 @@
+// Shared device helpers and launch plumbing for libflock_attn (gfx950, wave64).
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+#include "../../include/flock_attn.h"
+
+namespace flk {
+
+constexpr int kWave = 64;
+
+// ---------------------------------------------------------------- rounding --
+// The CPU oracle evaluates in f64 and rounds to f32 at fixed points. For +, -,
+// *, / and sqrt of two f32 operands, rounding the f64 result to f32 equals the
+// f32 operation itself (53 >= 2*24 + 2), so plain f32 arithmetic matches it.
+// Two compound forms need f64 on the device to match bit for bit:
+//   fma32(a, b, c) = f32(f64(a*b) + c): the f64 sum rounds before the f32 one.
+//   1/sqrt(y)      = f32(1 / sqrt(f64 y)): one f32 rounding of the compound.
+__device__ __forceinline__ float fma32(float a, float b, float c) {
+  return (float)((double)a * (double)b + (double)c);
+}
+__device__ __forceinline__ float rsqrt_once(float y) { return (float)(1.0 / sqrt((double)y)); }
+
+// ------------------------------------------------------------- lane shuffles --
+__device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
+
+// Sum over aligned groups of `width` lanes (width a power of two <= 64); every
+// lane of the group ends with the group total.
+template <int width>
+__device__ __forceinline__ float group_sum(float v) {
+#pragma unroll
+  for (int m = 1; m < width; m <<= 1) v += shfl_xor(v, m);
+  return v;
+}
+
+// --------------------------------------------------------- RoPE + RMSNorm ----
+// One wave owns one head vector of D (64 or 128) floats: lane l holds element
+// l and, for D = 128, element l + 64. The sum of squares follows the reference
+// kernel's order exactly (rmsnorm.wgsl:45-66, rmsnormRef ops_ref.ts:20-49 with
+// wg = 128): partial[t] = x_t^2 (one element per partial), then a pairwise
+// tree with strides 64, 32, ..., 1. Stride 64 is in-lane; the rest is an xor
+// butterfly, after which every lane holds the tree total (each level's value
+// in lane i equals tree[i mod stride], and addition is commutative).
+template <int D>
+__device__ __forceinline__ void head_rmsnorm(float& e0, float& e1, const float* __restrict__ g,
+                                             int lane, float eps) {
+  float p = e0 * e0;
+  if (D == 128) p = p + e1 * e1;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) p = p + shfl_xor(p, m);
+  // rmsnorm.wgsl:68 with the reference's rounding: fr(fr(sum / n) + eps), then
+  // 1/sqrt as one rounding (ops_ref.ts:39-45).
+  const float mean = p / (float)D;
+  const float scale = rsqrt_once(mean + eps);
+  if (lane < D) e0 = (e0 * scale) * g[lane];
+  if (D == 128) e1 = (e1 * scale) * g[lane + 64];
+}
+
+// One rotated element: `x` is this element, `y` its pair partner, `first`
+// says whether this element is the pair's a (else b). theta = fr(pos *
+// inv_freq[j]); cos/sin in f64 rounded once, like the oracle's
+// fr(Math.cos(theta)); a' = fr(-b*s + fr(a*c)) and b' = fr(b*c + fr(a*s)) with
+// the f64 sum rounding before the f32 one (ops_ref.ts:80-88).
+__device__ __forceinline__ float rope_elem(float x, float y, bool first, float inv_f, int pos) {
+  const float theta = (float)pos * inv_f;
+  const float c = (float)cos((double)theta);
+  const float s = (float)sin((double)theta);
+  if (first) return (float)(-(double)y * (double)s + (double)(x * c));
+  return (float)((double)x * (double)c + (double)(y * s));
+}
+
+// RoPE on one head vector held as above, at absolute position `pos`
+// (rope.wgsl:50-78, ropeRef ops_ref.ts:65-92). NEOX pairs (j, j + D/2): for
+// D = 128 both halves sit in the same lane; for D = 64 the partner is lane
+// l ^ 32. NORM pairs (2j, 2j+1): the partner is lane l ^ 1.
+template <int D>
+__device__ __forceinline__ void head_rope(float& e0, float& e1, const float* __restrict__ inv_freq,
+                                          int pos, int pairing, int lane) {
+  constexpr int half = D / 2;
+  if (pairing == FLK_ROPE_NORM) {
+    const float p0 = shfl_xor(e0, 1);
+    const float p1 = (D == 128) ? shfl_xor(e1, 1) : 0.f;
+    const bool first = (lane & 1) == 0;
+    if (lane < D) e0 = rope_elem(e0, p0, first, inv_freq[lane >> 1], pos);
+    if (D == 128) e1 = rope_elem(e1, p1, first, inv_freq[(lane + 64) >> 1], pos);
+  } else if (D == 128) {
+    const float a = e0, b = e1;  // elements j = lane and j + 64
+    e0 = rope_elem(a, b, true, inv_freq[lane], pos);
+    e1 = rope_elem(b, a, false, inv_freq[lane], pos);
+  } else {
+    const float p0 = shfl_xor(e0, 32);
+    const bool first = lane < half;
+    e0 = rope_elem(e0, p0, first, inv_freq[first ? lane : lane - half], pos);
+  }
+}
+
+// ---------------------------------------------------------------- launches --
+struct Stream {
+  static hipStream_t get();
+};
+
+// Internal launchers (return a hipError_t; the C ABI maps it to FLK_ERR_HIP).
+hipError_t launch_rmsnorm(const float* x, const float* g, float* o, uint32_t n, uint32_t n_vecs,
+                          float eps, hipStream_t st);
+hipError_t launch_rope(float* x, const float* inv_freq, uint32_t n_tokens, uint32_t n_heads,
+                       uint32_t head_dim, uint32_t pos0, int32_t pairing, hipStream_t st);
+hipError_t launch_kv_append(const float* kn, const float* v, float* kcache, float* vcache,
+                            uint32_t n_tokens, uint32_t pos0, uint32_t n_kv_heads,
+                            uint32_t head_dim, hipStream_t st);
+hipError_t launch_qk_prologue(const float* q_raw, const float* k_raw, const float* v_raw,
+                              const float* gq, const float* gk, const float* inv_freq, float eps,
+                              int32_t pairing, float* qn_out, float* kcache, float* vcache,
+                              uint32_t n_tokens, uint32_t pos0, uint32_t n_heads,
+                              uint32_t n_kv_heads, uint32_t head_dim, hipStream_t st);
+
+// Decode: plan + launch. `fused` carries the prologue inputs for
+// flk_decode_layer (null q_raw means plain decode).
+struct DecodeFused {
+  const float* q_raw = nullptr;
+  const float* k_raw = nullptr;
+  const float* v_raw = nullptr;
+  const float* gq = nullptr;
+  const float* gk = nullptr;
+  const float* inv_freq = nullptr;
+  float eps = 0.f;
+  int32_t pairing = 0;
+  float* qn_out = nullptr;
+  float* kcache_w = nullptr;
+  float* vcache_w = nullptr;
+};
+
+struct DecodeShape {
+  uint32_t n_heads, n_kv_heads, head_dim;
+  uint32_t n_seqs;      // 1 unless ragged
+  uint32_t max_n_keys;  // n_keys for a single sequence
+};
+
+uint32_t decode_keys_per_split(const DecodeShape& s);
+uint64_t decode_ws_bytes(const DecodeShape& s);
+uint64_t decode_ws_bound(const DecodeShape& s);
+hipError_t launch_decode(const float* q, const float* kcache, const float* vcache, float* o,
+                         const uint64_t* seq_row_off, const uint32_t* n_keys_dev,
+                         const DecodeShape& s, const DecodeFused* fused, void* ws, hipStream_t st);
+
+struct PrefillPlan {
+  uint32_t rows_per_tile;   // 128: query-head rows sharing one kv head
+  uint32_t q_per_tile;      // rows_per_tile / group
+  uint32_t n_qtiles;
+  uint32_t ktiles_per_split;
+  uint32_t max_splits;      // splits of the heaviest q-tile
+  uint64_t partial_slots;   // n_qtiles * max_splits * n_kv_heads
+};
+PrefillPlan prefill_plan(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                         uint32_t n_queries, uint32_t pos0);
+uint64_t prefill_ws_bytes(const PrefillPlan& p, uint32_t head_dim);
+uint64_t prefill_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                          uint32_t max_queries, uint32_t max_keys);
+hipError_t launch_prefill(const float* q, const float* kcache, const float* vcache, float* o,
+                          uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                          uint32_t n_queries, uint32_t pos0, void* ws, hipStream_t st);
+
+// Workspace layout: [counters: kCounterBytes][partials ...]. Counters are
+// uint32 and are returned to zero by the kernels that use them.
+constexpr uint64_t kCounterBytes = 64 * 1024;
+constexpr uint64_t kMaxCounters = kCounterBytes / 4;
+
+}  // namespace flk

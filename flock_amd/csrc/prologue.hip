@@ -1,0 +1,152 @@
+// Per-head RMSNorm + RoPE + K/V append, and the unfused rmsnorm / rope / append
+// ops. These are bytes-trivial kernels (a few KB per token); their job is to
+// be bit-exact with the CPU oracle so that the KV cache a prefill writes is the
+// cache N decode steps write (test_prefill.ts:119-132).
+#include "common.hpp"
+
+namespace flk {
+
+// ------------------------------------------------------------ rmsnorm (any n)
+// rmsnorm.wgsl:41-73: one 128-thread workgroup per vector; thread t sums a
+// stride-128 slice with fma32, then a pairwise LDS tree (strides 64 .. 1).
+__global__ __launch_bounds__(128) void rmsnorm_kernel(const float* __restrict__ x,
+                                                      const float* __restrict__ g,
+                                                      float* __restrict__ o, uint32_t n,
+                                                      uint32_t n_vecs, float eps) {
+  __shared__ float part[128];
+  const uint32_t vec = blockIdx.x;
+  const uint32_t t = threadIdx.x;
+  if (vec >= n_vecs) return;  // uniform per block
+  const float* xv = x + (size_t)vec * n;
+  float acc = 0.f;
+  for (uint32_t i = t; i < n; i += 128) acc = fma32(xv[i], xv[i], acc);
+  part[t] = acc;
+  __syncthreads();
+  for (uint32_t stride = 64; stride > 0; stride >>= 1) {
+    if (t < stride) part[t] = part[t] + part[t + stride];
+    __syncthreads();
+  }
+  const float mean = part[0] / (float)n;
+  const float scale = rsqrt_once(mean + eps);
+  float* ov = o + (size_t)vec * n;
+  for (uint32_t i = t; i < n; i += 128) ov[i] = (xv[i] * scale) * g[i];
+}
+
+hipError_t launch_rmsnorm(const float* x, const float* g, float* o, uint32_t n, uint32_t n_vecs,
+                          float eps, hipStream_t st) {
+  hipLaunchKernelGGL(rmsnorm_kernel, dim3(n_vecs), dim3(128), 0, st, x, g, o, n, n_vecs, eps);
+  return hipGetLastError();
+}
+
+// ------------------------------------------------------------- rope (any d)
+// rope.wgsl:50-78: one thread per rotated pair, in place.
+__global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x,
+                                                   const float* __restrict__ inv_freq,
+                                                   uint32_t n_tokens, uint32_t n_heads,
+                                                   uint32_t head_dim, uint32_t pos0,
+                                                   int32_t pairing) {
+  const uint32_t half = head_dim / 2;
+  const uint64_t total = (uint64_t)n_tokens * n_heads * half;
+  const uint64_t gid = (uint64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= total) return;
+  const uint32_t j = (uint32_t)(gid % half);
+  const uint32_t head = (uint32_t)((gid / half) % n_heads);
+  const uint32_t token = (uint32_t)(gid / ((uint64_t)half * n_heads));
+  const size_t base = ((size_t)token * n_heads + head) * head_dim;
+  const size_t ia = base + (pairing == FLK_ROPE_NORM ? 2 * j : j);
+  const size_t ib = base + (pairing == FLK_ROPE_NORM ? 2 * j + 1 : j + half);
+  const float a = x[ia], b = x[ib];
+  const int pos = (int)(pos0 + token);
+  x[ia] = rope_elem(a, b, true, inv_freq[j], pos);
+  x[ib] = rope_elem(b, a, false, inv_freq[j], pos);
+}
+
+hipError_t launch_rope(float* x, const float* inv_freq, uint32_t n_tokens, uint32_t n_heads,
+                       uint32_t head_dim, uint32_t pos0, int32_t pairing, hipStream_t st) {
+  const uint64_t total = (uint64_t)n_tokens * n_heads * (head_dim / 2);
+  const uint32_t blocks = (uint32_t)((total + 255) / 256);
+  hipLaunchKernelGGL(rope_kernel, dim3(blocks), dim3(256), 0, st, x, inv_freq, n_tokens, n_heads,
+                     head_dim, pos0, pairing);
+  return hipGetLastError();
+}
+
+// ---------------------------------------------------------------- append ----
+// layer.ts:616-622 / 737-741: both caches are [key][kv_head][head_dim], so n
+// tokens of new rows are one contiguous run at row pos0.
+hipError_t launch_kv_append(const float* kn, const float* v, float* kcache, float* vcache,
+                            uint32_t n_tokens, uint32_t pos0, uint32_t n_kv_heads,
+                            uint32_t head_dim, hipStream_t st) {
+  const size_t row = (size_t)n_kv_heads * head_dim;
+  const size_t bytes = (size_t)n_tokens * row * sizeof(float);
+  hipError_t e = hipMemcpyAsync(kcache + (size_t)pos0 * row, kn, bytes, hipMemcpyDeviceToDevice, st);
+  if (e != hipSuccess) return e;
+  return hipMemcpyAsync(vcache + (size_t)pos0 * row, v, bytes, hipMemcpyDeviceToDevice, st);
+}
+
+// --------------------------------------------------------- fused prologue ----
+// One wave per head vector. Vector id -> (token, kind): the first n_heads are
+// q heads (norm + rope -> qn_out), the next n_kv_heads are k heads (norm + rope
+// -> kcache row pos0 + token), the last n_kv_heads are v heads (copied raw to
+// vcache). Identical arithmetic to rmsnorm_kernel + rope_kernel for head_dim
+// vectors, so the caches match the unfused path bit for bit.
+template <int D>
+__global__ __launch_bounds__(256) void qk_prologue_kernel(
+    const float* __restrict__ q_raw, const float* __restrict__ k_raw,
+    const float* __restrict__ v_raw, const float* __restrict__ gq, const float* __restrict__ gk,
+    const float* __restrict__ inv_freq, float eps, int32_t pairing, float* __restrict__ qn_out,
+    float* __restrict__ kcache, float* __restrict__ vcache, uint32_t n_tokens, uint32_t pos0,
+    uint32_t n_heads, uint32_t n_kv_heads) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t per_tok = n_heads + 2 * n_kv_heads;
+  const uint64_t vec = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
+  if (vec >= (uint64_t)n_tokens * per_tok) return;  // uniform per wave
+  const uint32_t tok = (uint32_t)(vec / per_tok);
+  const uint32_t idx = (uint32_t)(vec % per_tok);
+  const uint32_t pos = pos0 + tok;
+  const size_t kv_row = (size_t)n_kv_heads * D;
+  const float* src;
+  float* dst;
+  const float* g = nullptr;
+  if (idx < n_heads) {
+    src = q_raw + ((size_t)tok * n_heads + idx) * D;
+    dst = qn_out + ((size_t)tok * n_heads + idx) * D;
+    g = gq;
+  } else if (idx < n_heads + n_kv_heads) {
+    const uint32_t h = idx - n_heads;
+    src = k_raw + (size_t)tok * kv_row + (size_t)h * D;
+    dst = kcache + (size_t)pos * kv_row + (size_t)h * D;
+    g = gk;
+  } else {
+    const uint32_t h = idx - n_heads - n_kv_heads;
+    src = v_raw + (size_t)tok * kv_row + (size_t)h * D;
+    dst = vcache + (size_t)pos * kv_row + (size_t)h * D;
+  }
+  float e0 = lane < D ? src[lane] : 0.f;
+  float e1 = D == 128 ? src[lane + 64] : 0.f;
+  if (g != nullptr) {  // uniform per wave
+    head_rmsnorm<D>(e0, e1, g, lane, eps);
+    head_rope<D>(e0, e1, inv_freq, (int)pos, pairing, lane);
+  }
+  if (lane < D) dst[lane] = e0;
+  if (D == 128) dst[lane + 64] = e1;
+}
+
+hipError_t launch_qk_prologue(const float* q_raw, const float* k_raw, const float* v_raw,
+                              const float* gq, const float* gk, const float* inv_freq, float eps,
+                              int32_t pairing, float* qn_out, float* kcache, float* vcache,
+                              uint32_t n_tokens, uint32_t pos0, uint32_t n_heads,
+                              uint32_t n_kv_heads, uint32_t head_dim, hipStream_t st) {
+  const uint64_t vecs = (uint64_t)n_tokens * (n_heads + 2 * n_kv_heads);
+  const uint32_t blocks = (uint32_t)((vecs + 3) / 4);
+  if (head_dim == 128)
+    hipLaunchKernelGGL(qk_prologue_kernel<128>, dim3(blocks), dim3(256), 0, st, q_raw, k_raw,
+                       v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache, vcache, n_tokens,
+                       pos0, n_heads, n_kv_heads);
+  else
+    hipLaunchKernelGGL(qk_prologue_kernel<64>, dim3(blocks), dim3(256), 0, st, q_raw, k_raw,
+                       v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache, vcache, n_tokens,
+                       pos0, n_heads, n_kv_heads);
+  return hipGetLastError();
+}
+
+}  // namespace flk

@@ -1,0 +1,199 @@
+"""Python wrappers over the C ABI: device buffers, workspace, stream, and one
+function per entry point of include/flock_attn.h.
+
+Device arrays may be passed as a DeviceBuffer, a raw device pointer (int), or a
+contiguous device tensor exposing ``data_ptr()`` (e.g. a torch tensor on the
+GPU). Shapes are the reference's flat layouts (see flock_attn.h).
+"""
+from __future__ import annotations
+
+import ctypes
+import math
+
+import numpy as np
+
+from ._lib import ROPE_NEOX, ROPE_NORM, FlockError, check, lib
+
+PAIRING = {"neox": ROPE_NEOX, "norm": ROPE_NORM}
+
+
+def _pairing(p) -> int:
+    if isinstance(p, str):
+        if p not in PAIRING:
+            raise ValueError(f"rope pairing must be 'neox' or 'norm', got {p!r}")
+        return PAIRING[p]
+    return int(p)
+
+
+class DeviceBuffer:
+    """Device memory from flk_alloc (the reference's storageBuffer)."""
+
+    def __init__(self, nbytes: int):
+        if nbytes <= 0:
+            raise ValueError("DeviceBuffer needs a positive size")
+        p = ctypes.c_void_p()
+        check(lib().flk_alloc(ctypes.byref(p), nbytes), "flk_alloc")
+        self.ptr = p.value
+        self.nbytes = nbytes
+
+    @classmethod
+    def from_array(cls, a: np.ndarray) -> "DeviceBuffer":
+        a = np.ascontiguousarray(a)
+        b = cls(max(a.nbytes, 4))
+        b.upload(a)
+        return b
+
+    def upload(self, a: np.ndarray, offset_bytes: int = 0) -> None:
+        a = np.ascontiguousarray(a)
+        if offset_bytes + a.nbytes > self.nbytes:
+            raise ValueError(f"upload of {a.nbytes} B at {offset_bytes} overruns {self.nbytes} B")
+        check(lib().flk_h2d(self.ptr, a.ctypes.data, a.nbytes, offset_bytes), "flk_h2d")
+
+    def download(self, count: int, dtype=np.float32, offset_bytes: int = 0) -> np.ndarray:
+        out = np.empty(count, dtype)
+        if offset_bytes + out.nbytes > self.nbytes:
+            raise ValueError("download overruns the buffer")
+        check(lib().flk_d2h(out.ctypes.data, self.ptr, out.nbytes, offset_bytes), "flk_d2h")
+        return out
+
+    def zero(self) -> None:
+        check(lib().flk_memset(self.ptr, 0, self.nbytes), "flk_memset")
+
+    def free(self) -> None:
+        if getattr(self, "ptr", None):
+            lib().flk_free(self.ptr)
+            self.ptr = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+def ptr(x) -> int | None:
+    """Device address of a DeviceBuffer, int pointer or device tensor."""
+    if x is None:
+        return None
+    if isinstance(x, DeviceBuffer):
+        return x.ptr
+    if isinstance(x, int):
+        return x
+    if hasattr(x, "data_ptr"):
+        if getattr(x, "is_cuda", True) is False:
+            raise ValueError("host tensor passed where a device array is required")
+        if hasattr(x, "is_contiguous") and not x.is_contiguous():
+            raise ValueError("device tensor must be contiguous")
+        return int(x.data_ptr())
+    raise TypeError(f"cannot take a device pointer of {type(x).__name__}")
+
+
+def workspace_bytes(n_heads: int, n_kv_heads: int, head_dim: int, max_keys: int,
+                    max_queries: int = 0, max_seqs: int = 1) -> int:
+    n = lib().flk_workspace_bytes(n_heads, n_kv_heads, head_dim, max_keys, max_queries, max_seqs)
+    if n == 0:
+        raise FlockError(-1, "invalid shape for flk_workspace_bytes")
+    return int(n)
+
+
+class Workspace(DeviceBuffer):
+    """Split-K scratch: sized by flk_workspace_bytes, counters zeroed once."""
+
+    def __init__(self, n_heads: int, n_kv_heads: int, head_dim: int, max_keys: int,
+                 max_queries: int = 0, max_seqs: int = 1):
+        super().__init__(workspace_bytes(n_heads, n_kv_heads, head_dim, max_keys, max_queries,
+                                         max_seqs))
+        check(lib().flk_workspace_init(self.ptr, self.nbytes), "flk_workspace_init")
+
+
+def set_stream(stream) -> None:
+    """Launch on ``stream``: a hipStream_t (int), a torch stream, or None."""
+    if stream is None:
+        h = None
+    elif isinstance(stream, int):
+        h = stream
+    else:
+        h = int(stream.cuda_stream)
+    check(lib().flk_set_stream(h), "flk_set_stream")
+
+
+def sync() -> None:
+    check(lib().flk_sync(), "flk_sync")
+
+
+def device_count() -> int:
+    n = ctypes.c_int32(0)
+    check(lib().flk_device_count(ctypes.byref(n)))
+    return n.value
+
+
+def rope_inv_freq(head_dim: int, base: float) -> np.ndarray:
+    """inv_freq[j] = f32(1 / base^(2j/d)) on the host (kernels/layer.ts:180-186)."""
+    return np.array([1.0 / math.pow(base, (2.0 * j) / head_dim) for j in range(head_dim // 2)],
+                    dtype=np.float32)
+
+
+def _ws(ws) -> tuple[int, int]:
+    if ws is None:
+        return None, 0
+    if isinstance(ws, DeviceBuffer):
+        return ws.ptr, ws.nbytes
+    p, n = ws
+    return ptr(p), int(n)
+
+
+def rmsnorm(x, g, o, n: int, n_vecs: int, eps: float) -> None:
+    check(lib().flk_rmsnorm(ptr(x), ptr(g), ptr(o), n, n_vecs, eps), "flk_rmsnorm")
+
+
+def rope(x, inv_freq, n_tokens: int, n_heads: int, head_dim: int, pos0: int,
+         pairing="neox") -> None:
+    check(lib().flk_rope(ptr(x), ptr(inv_freq), n_tokens, n_heads, head_dim, pos0,
+                         _pairing(pairing)), "flk_rope")
+
+
+def kv_append(kn, v, kcache, vcache, n_tokens: int, pos0: int, n_kv_heads: int, head_dim: int,
+              max_keys: int) -> None:
+    check(lib().flk_kv_append(ptr(kn), ptr(v), ptr(kcache), ptr(vcache), n_tokens, pos0,
+                              n_kv_heads, head_dim, max_keys), "flk_kv_append")
+
+
+def qk_prologue(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps: float, pairing, qn_out, kcache,
+                vcache, n_tokens: int, pos0: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                max_keys: int) -> None:
+    check(lib().flk_qk_prologue(ptr(q_raw), ptr(k_raw), ptr(v_raw), ptr(gq), ptr(gk),
+                                ptr(inv_freq), eps, _pairing(pairing), ptr(qn_out), ptr(kcache),
+                                ptr(vcache), n_tokens, pos0, n_heads, n_kv_heads, head_dim,
+                                max_keys), "flk_qk_prologue")
+
+
+def attn_decode(q, kcache, vcache, o, n_heads: int, n_kv_heads: int, head_dim: int,
+                n_keys: int, ws) -> None:
+    w, nb = _ws(ws)
+    check(lib().flk_attn_decode(ptr(q), ptr(kcache), ptr(vcache), ptr(o), n_heads, n_kv_heads,
+                                head_dim, n_keys, w, nb), "flk_attn_decode")
+
+
+def attn_prefill(q, kcache, vcache, o, n_heads: int, n_kv_heads: int, head_dim: int,
+                 n_queries: int, pos0: int, ws) -> None:
+    w, nb = _ws(ws)
+    check(lib().flk_attn_prefill(ptr(q), ptr(kcache), ptr(vcache), ptr(o), n_heads, n_kv_heads,
+                                 head_dim, n_queries, pos0, w, nb), "flk_attn_prefill")
+
+
+def decode_layer(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps: float, pairing, qn_out, kcache,
+                 vcache, o, pos: int, n_heads: int, n_kv_heads: int, head_dim: int,
+                 max_keys: int, ws) -> None:
+    w, nb = _ws(ws)
+    check(lib().flk_decode_layer(ptr(q_raw), ptr(k_raw), ptr(v_raw), ptr(gq), ptr(gk),
+                                 ptr(inv_freq), eps, _pairing(pairing), ptr(qn_out), ptr(kcache),
+                                 ptr(vcache), ptr(o), pos, n_heads, n_kv_heads, head_dim,
+                                 max_keys, w, nb), "flk_decode_layer")
+
+
+def attn_decode_ragged(q, kcache, vcache, seq_row_off, n_keys, o, n_seqs: int, max_n_keys: int,
+                       n_heads: int, n_kv_heads: int, head_dim: int, ws) -> None:
+    w, nb = _ws(ws)
+    check(lib().flk_attn_decode_ragged(ptr(q), ptr(kcache), ptr(vcache), ptr(seq_row_off),
+                                       ptr(n_keys), ptr(o), n_seqs, max_n_keys, n_heads,
+                                       n_kv_heads, head_dim, w, nb), "flk_attn_decode_ragged")

@@ -1,0 +1,202 @@
+"""CPU oracle for flock's attention hot path -- TEST INFRASTRUCTURE ONLY.
+
+Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline leg may import
+this package, and only as the checker. The product (flock_amd) never imports it.
+
+Two independent formulations live here:
+
+* ``flock_oracle.c`` (wrapped below): the reference's strict-f32 CPU oracle
+  restated rounding point for rounding point (kernels/ops_ref.ts,
+  kernels/head_ref.ts, kernels/layer_ref.ts, kernels/lib.ts:169-171).
+* ``closed_form``: textbook float64 formulas (softmax(q k^T / sqrt d) v with
+  the GQA map and causal bound, RMSNorm, rotation) used to pin the
+  restatement. They share no code with it.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import subprocess
+
+import numpy as np
+
+_HERE = os.path.dirname(os.path.abspath(__file__))
+_LIB_PATH = os.path.join(_HERE, "libflock_oracle.so")
+_lib = None
+
+NEOX, NORM = 0, 1
+PAIRING = {"neox": NEOX, "norm": NORM}
+# qwen3.attention.layer_norm_rms_epsilon as the f32 the reference uploads
+# (kernels/layer.ts:124).
+QWEN3_EPS = 9.999999974752427e-7
+QWEN3_ROPE_BASE = 1e6
+
+_f32p = ctypes.POINTER(ctypes.c_float)
+
+
+def build() -> str:
+    """Compile flock_oracle.c with oracle/Makefile (gcc, strict IEEE)."""
+    subprocess.run(["make", "-s", "-C", _HERE], check=True)
+    return _LIB_PATH
+
+
+def lib() -> ctypes.CDLL:
+    global _lib
+    if _lib is None:
+        if not os.path.exists(_LIB_PATH):
+            build()
+        L = ctypes.CDLL(_LIB_PATH)
+        i, d, i64 = ctypes.c_int, ctypes.c_double, ctypes.c_int64
+        sig = {
+            "flko_rmsnorm": (None, [_f32p, _f32p, _f32p, i, i, d, i]),
+            "flko_rope": (None, [_f32p, i, i, i, i, _f32p, i]),
+            "flko_rope_inv_freq": (None, [i, d, _f32p]),
+            "flko_attn": (None, [_f32p, _f32p, _f32p, _f32p, i, i, i, i]),
+            "flko_attn_prefill": (None, [_f32p, _f32p, _f32p, _f32p, i, i, i, i, i, i, i]),
+            "flko_argmax": (i, [_f32p, i]),
+            "flko_rel_err": (d, [_f32p, _f32p, i64, d]),
+            "flko_abs_err_scaled": (d, [_f32p, _f32p, i64, d]),
+            "flko_amax": (d, [_f32p, i64]),
+            "flko_layer_attn_decode": (
+                None,
+                [_f32p] * 6 + [d, i] + [_f32p] * 4 + [i, i, i, i],
+            ),
+            "flko_layer_attn_prefill": (
+                None,
+                [_f32p] * 6 + [d, i] + [_f32p] * 4 + [i, i, i, i, i],
+            ),
+            "flko_set_threads": (i, [i]),
+        }
+        for name, (res, args) in sig.items():
+            fn = getattr(L, name)
+            fn.restype = res
+            fn.argtypes = args
+        _lib = L
+    return _lib
+
+
+def _f32(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.float32)
+
+
+def _p(a: np.ndarray):
+    return a.ctypes.data_as(_f32p)
+
+
+def set_threads(n: int) -> int:
+    """Threads for the oracle's parallel loops (heads / query-head pairs)."""
+    return lib().flko_set_threads(int(n))
+
+
+def rmsnorm(x, g, n: int, n_vecs: int, eps: float = QWEN3_EPS, wg: int = 128) -> np.ndarray:
+    """rmsnormRef, kernels/ops_ref.ts:20-49."""
+    x, g = _f32(x), _f32(g)
+    assert x.size == n * n_vecs and g.size == n and wg & (wg - 1) == 0
+    o = np.empty(n * n_vecs, np.float32)
+    lib().flko_rmsnorm(_p(x), _p(g), _p(o), n, n_vecs, float(eps), wg)
+    return o
+
+
+def rope(x, n_tokens: int, n_heads: int, head_dim: int, pos0: int, inv_freq,
+         pairing: str = "neox") -> np.ndarray:
+    """ropeRef, kernels/ops_ref.ts:65-92 (returns a rotated copy)."""
+    out = _f32(x).copy()
+    inv = _f32(inv_freq)
+    assert out.size == n_tokens * n_heads * head_dim and inv.size == head_dim // 2
+    lib().flko_rope(_p(out), n_tokens, n_heads, head_dim, pos0, _p(inv), PAIRING[pairing])
+    return out
+
+
+def rope_inv_freq(head_dim: int, base: float = QWEN3_ROPE_BASE) -> np.ndarray:
+    """ropeInvFreq, kernels/ops_ref.ts:95-100."""
+    out = np.empty(head_dim // 2, np.float32)
+    lib().flko_rope_inv_freq(head_dim, float(base), _p(out))
+    return out
+
+
+def attn(q, k, v, n_heads: int, n_kv_heads: int, head_dim: int, n_keys: int) -> np.ndarray:
+    """attnRef, kernels/ops_ref.ts:135-174."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    assert q.size == n_heads * head_dim
+    assert k.size >= n_keys * n_kv_heads * head_dim and v.size >= n_keys * n_kv_heads * head_dim
+    o = np.empty(n_heads * head_dim, np.float32)
+    lib().flko_attn(_p(q), _p(k), _p(v), _p(o), n_heads, n_kv_heads, head_dim, n_keys)
+    return o
+
+
+def attn_prefill(q, k, v, n_heads: int, n_kv_heads: int, head_dim: int, n_queries: int,
+                 pos0: int, tile: int = 64, wg: int = 128) -> np.ndarray:
+    """attnPrefillRef, kernels/head_ref.ts:99-183."""
+    q, k, v = _f32(q), _f32(k), _f32(v)
+    n_keys = pos0 + n_queries
+    assert q.size == n_queries * n_heads * head_dim
+    assert k.size >= n_keys * n_kv_heads * head_dim and v.size >= n_keys * n_kv_heads * head_dim
+    o = np.empty(n_queries * n_heads * head_dim, np.float32)
+    lib().flko_attn_prefill(_p(q), _p(k), _p(v), _p(o), n_heads, n_kv_heads, head_dim,
+                            n_queries, pos0, tile, wg)
+    return o
+
+
+def argmax(x) -> int:
+    """argmaxRef, kernels/head_ref.ts:65-74 (lowest index wins ties)."""
+    x = _f32(x)
+    return int(lib().flko_argmax(_p(x), x.size))
+
+
+def rel_err(a, b, floor: float = 1e-6) -> float:
+    """relErr, kernels/ops_ref.ts:185-191."""
+    a, b = _f32(a), _f32(b)
+    assert a.size == b.size
+    return float(lib().flko_rel_err(_p(a), _p(b), a.size, floor))
+
+
+def abs_err_scaled(a, b, scale: float) -> float:
+    """absErrScaled, kernels/ops_ref.ts:206-210."""
+    a, b = _f32(a), _f32(b)
+    assert a.size == b.size
+    return float(lib().flko_abs_err_scaled(_p(a), _p(b), a.size, float(scale)))
+
+
+def amax(a) -> float:
+    """amax, kernels/ops_ref.ts:213-217."""
+    a = _f32(a)
+    return float(lib().flko_amax(_p(a), a.size))
+
+
+def layer_attn_decode(q_raw, k_raw, v_raw, gq, gk, inv_freq, kcache: np.ndarray,
+                      vcache: np.ndarray, pos: int, n_heads: int, n_kv_heads: int,
+                      head_dim: int, eps: float = QWEN3_EPS, pairing: str = "neox"):
+    """Attention slice of layerForwardRef, kernels/layer_ref.ts:46-70.
+
+    Appends row ``pos`` to ``kcache``/``vcache`` (float32, modified in place) and
+    returns ``(qn, o)``.
+    """
+    assert kcache.dtype == np.float32 and kcache.flags.c_contiguous
+    assert vcache.dtype == np.float32 and vcache.flags.c_contiguous
+    assert kcache.size >= (pos + 1) * n_kv_heads * head_dim
+    args = [_f32(a) for a in (q_raw, k_raw, v_raw, gq, gk, inv_freq)]
+    qn = np.empty(n_heads * head_dim, np.float32)
+    o = np.empty(n_heads * head_dim, np.float32)
+    lib().flko_layer_attn_decode(*[_p(a) for a in args], float(eps), PAIRING[pairing],
+                                 _p(kcache), _p(vcache), _p(qn), _p(o), pos, n_heads,
+                                 n_kv_heads, head_dim)
+    return qn, o
+
+
+def layer_attn_prefill(q_raw, k_raw, v_raw, gq, gk, inv_freq, kcache: np.ndarray,
+                       vcache: np.ndarray, n: int, pos0: int, n_heads: int, n_kv_heads: int,
+                       head_dim: int, eps: float = QWEN3_EPS, pairing: str = "neox"):
+    """Attention slice of layerPrefillRef, kernels/layer_ref.ts:137-165.
+
+    Appends rows ``pos0 .. pos0+n-1`` to the caches in place; returns ``(qn, o)``.
+    """
+    assert kcache.dtype == np.float32 and kcache.flags.c_contiguous
+    assert vcache.dtype == np.float32 and vcache.flags.c_contiguous
+    assert kcache.size >= (pos0 + n) * n_kv_heads * head_dim
+    args = [_f32(a) for a in (q_raw, k_raw, v_raw, gq, gk, inv_freq)]
+    qn = np.empty(n * n_heads * head_dim, np.float32)
+    o = np.empty(n * n_heads * head_dim, np.float32)
+    lib().flko_layer_attn_prefill(*[_p(a) for a in args], float(eps), PAIRING[pairing],
+                                  _p(kcache), _p(vcache), _p(qn), _p(o), n, pos0, n_heads,
+                                  n_kv_heads, head_dim)
+    return qn, o

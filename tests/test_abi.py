@@ -1,0 +1,123 @@
+"""The drop-in boundary, checked without a GPU.
+
+* libflock_attn.so loads and exports every function include/flock_attn.h
+  declares, and the ctypes table in flock_amd/_lib.py binds exactly that set.
+* Host-side guards run before any launch and return the documented status
+  (the reference throws from Layer before encoding: layer.ts:575, 689-698;
+  lib.ts:504-506). Garbage non-null pointers are safe here because a rejected
+  call never dereferences them.
+"""
+from __future__ import annotations
+
+import ctypes
+import os
+import re
+
+import pytest
+
+from flock_amd import _lib
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+HEADER = os.path.join(ROOT, "include", "flock_attn.h")
+FAKE = 0x1000  # never dereferenced: every call below fails validation first
+
+
+def declared_functions() -> set[str]:
+    text = open(HEADER).read()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return set(re.findall(r"\b(flk_\w+)\s*\(", text))
+
+
+def test_header_and_binding_agree():
+    assert declared_functions() == set(_lib.SIGNATURES)
+
+
+def test_library_exports_every_declared_symbol():
+    L = _lib.lib()
+    for name in declared_functions():
+        assert hasattr(L, name), name
+    out = os.popen(f"nm -D --defined-only {_lib.LIB_PATH}").read()
+    exported = set(re.findall(r"\b(flk_\w+)$", out, flags=re.M))
+    assert declared_functions() <= exported
+
+
+def test_version_and_empty_error():
+    L = _lib.lib()
+    assert b"gfx950" in L.flk_version()
+
+
+def code_and_msg(rc):
+    return rc, _lib.lib().flk_last_error().decode()
+
+
+def test_decode_layer_cache_full_is_rejected_before_launch():
+    L = _lib.lib()
+    rc, msg = code_and_msg(L.flk_decode_layer(*([FAKE] * 6), 1e-6, 0, *([FAKE] * 4),
+                                              2048, 16, 8, 128, 2048, FAKE, 1 << 30))
+    assert rc == _lib.FLK_ERR_CACHE_FULL and "2048" in msg
+
+
+def test_prologue_cache_overflow_is_rejected():
+    L = _lib.lib()
+    rc, msg = code_and_msg(L.flk_qk_prologue(*([FAKE] * 6), 1e-6, 0, *([FAKE] * 3),
+                                             5, 2046, 16, 8, 128, 2048))
+    assert rc == _lib.FLK_ERR_CACHE_FULL and "2046 + 5" in msg
+
+
+@pytest.mark.parametrize("H,Hkv,d,code", [(16, 8, 96, _lib.FLK_ERR_UNSUPPORTED),
+                                          (16, 6, 128, _lib.FLK_ERR_ARG),
+                                          (32, 2, 128, _lib.FLK_ERR_UNSUPPORTED),
+                                          (0, 8, 128, _lib.FLK_ERR_ARG)])
+def test_unsupported_shapes(H, Hkv, d, code):
+    L = _lib.lib()
+    rc = L.flk_attn_decode(FAKE, FAKE, FAKE, FAKE, H, Hkv, d, 10, FAKE, 1 << 30)
+    assert rc == code
+
+
+def test_null_pointer_and_zero_sizes():
+    L = _lib.lib()
+    assert L.flk_attn_decode(None, FAKE, FAKE, FAKE, 16, 8, 128, 10, FAKE, 1 << 30) == _lib.FLK_ERR_ARG
+    assert "q is null" in L.flk_last_error().decode()
+    assert L.flk_attn_decode(FAKE, FAKE, FAKE, FAKE, 16, 8, 128, 0, FAKE, 1 << 30) == _lib.FLK_ERR_ARG
+    assert L.flk_attn_prefill(FAKE, FAKE, FAKE, FAKE, 16, 8, 128, 0, 0, FAKE, 1 << 30) == _lib.FLK_ERR_ARG
+    assert L.flk_rmsnorm(FAKE, FAKE, FAKE, 0, 1, 1e-6) == _lib.FLK_ERR_ARG
+    assert L.flk_rope(FAKE, FAKE, 1, 1, 127, 0, 0) == _lib.FLK_ERR_ARG
+    assert L.flk_rope(FAKE, FAKE, 1, 1, 128, 0, 7) == _lib.FLK_ERR_ARG
+
+
+def test_workspace_checks():
+    L = _lib.lib()
+    need = L.flk_workspace_bytes(16, 8, 128, 32832, 0, 1)
+    assert need > 0
+    assert L.flk_attn_decode(FAKE, FAKE, FAKE, FAKE, 16, 8, 128, 32769, None, 0) == _lib.FLK_ERR_WORKSPACE
+    assert L.flk_attn_decode(FAKE, FAKE, FAKE, FAKE, 16, 8, 128, 32769, 0x1000, 16) == _lib.FLK_ERR_WORKSPACE
+    # Misaligned workspace.
+    assert L.flk_attn_decode(FAKE, FAKE, FAKE, FAKE, 16, 8, 128, 32769, 0x1004,
+                             need) == _lib.FLK_ERR_WORKSPACE
+
+
+def test_workspace_bytes_covers_every_call_in_range():
+    # A Layer sizes its workspace once from (maxKeys, maxPrefill); every call it
+    # can then make must fit. Checked with the per-call sizing query -- nothing
+    # is launched.
+    L = _lib.lib()
+    for H, Hkv in [(16, 8), (16, 16), (4, 1), (12, 4)]:
+        for maxk, maxp in [(2048, 512), (32832, 64), (4096, 2048), (100, 100), (40000, 2048)]:
+            ws = L.flk_workspace_bytes(H, Hkv, 128, maxk, maxp, 1)
+            for n in sorted({1, 2, 63, 64, 65, maxp // 2, maxp}):
+                for pos0 in sorted({0, 1, maxk // 3, maxk - 2 * n, maxk - n}):
+                    if n < 1 or n > maxp or pos0 < 0 or pos0 + n > maxk:
+                        continue
+                    need = L.flk_call_workspace_bytes(1, H, Hkv, 128, n, pos0, 1)
+                    assert 0 < need <= ws, (H, Hkv, maxk, maxp, n, pos0)
+            for nk in sorted({1, 2, min(511, maxk), maxk // 2, maxk}):
+                assert 0 < L.flk_call_workspace_bytes(0, H, Hkv, 128, nk, 0, 1) <= ws
+
+
+def test_ragged_workspace_bound():
+    L = _lib.lib()
+    for seqs in (1, 3, 64, 200):
+        ws = L.flk_workspace_bytes(16, 8, 128, 16385, 0, seqs)
+        for maxn in (1, 100, 1024, 5000, 16385):
+            for s in range(1, seqs + 1, max(1, seqs // 7)):
+                assert 0 < L.flk_call_workspace_bytes(2, 16, 8, 128, maxn, 0, s) <= ws

@@ -1,0 +1,197 @@
+"""The Layer mirror (flock_amd.layer) on the GPU: kernels/test_prefill.ts's
+checks with synthetic q/k/v in place of real Qwen3 weights (the reference's
+version fetches blk.24 from HuggingFace, which is unavailable offline).
+
+  * prefill of N vs the CPU layer reference (layer_ref.ts:137-165 slice);
+  * prefill of N == N decode steps: outputs within tolerance and a
+    BIT-IDENTICAL KV cache (test_prefill.ts:77-138);
+  * prefill then decode on top of it (test_prefill.ts:140-186);
+  * RoPE position is live at pos0 = 900 (test_prefill.ts:188-261);
+  * one prefill of 10 == two of 5 (test_prefill.ts:263-288);
+  * guard rails throw before touching the device (test_prefill.ts:290-308),
+    plus cache-full and desync.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from conftest import randn
+from parity import fmt, meets_bar, metrics
+
+pytestmark = pytest.mark.gpu
+
+layer_mod = pytest.importorskip("flock_amd.layer")
+Layer, LayerConfig = layer_mod.Layer, layer_mod.LayerConfig
+from flock_amd import CacheFullError  # noqa: E402
+
+CFG = LayerConfig(maxKeys=2048, maxPrefill=256)
+H, HKV, D = CFG.nHeads, CFG.nKvHeads, CFG.headDim
+
+
+def gains(rng):
+    return (rng.normal(1, 0.1, D).astype(np.float32), rng.normal(1, 0.1, D).astype(np.float32))
+
+
+def inputs(rng, n):
+    return randn(rng, n * H * D), randn(rng, n * HKV * D), randn(rng, n * HKV * D)
+
+
+def tok(a, i, width):
+    return a[i * width:(i + 1) * width]
+
+
+class RefLayer:
+    """The oracle's layer slice with its own growing cache (layer_ref.ts)."""
+
+    def __init__(self, gq, gk, cfg=CFG):
+        self.gq, self.gk, self.cfg = gq, gk, cfg
+        self.inv = oracle.rope_inv_freq(cfg.headDim, cfg.ropeBase)
+        self.kc = np.zeros(cfg.maxKeys * HKV * D, np.float32)
+        self.vc = np.zeros(cfg.maxKeys * HKV * D, np.float32)
+        self.n = 0
+
+    def prefill(self, n, q, k, v):
+        _, o = oracle.layer_attn_prefill(q, k, v, self.gq, self.gk, self.inv, self.kc, self.vc,
+                                         n, self.n, H, HKV, D)
+        self.n += n
+        return o
+
+    def decode(self, q, k, v):
+        _, o = oracle.layer_attn_decode(q, k, v, self.gq, self.gk, self.inv, self.kc, self.vc,
+                                        self.n, H, HKV, D)
+        self.n += 1
+        return o
+
+
+@pytest.mark.parametrize("n", [1, 2, 7, 13, 64, 65, 256])
+def test_prefill_vs_cpu_reference(rng, n):
+    gq, gk = gains(rng)
+    q, k, v = inputs(rng, n)
+    L = Layer.create(CFG, gq, gk)
+    L.encodePrefill(n, q, k, v)
+    got = L.readOutput(n)
+    ref = RefLayer(gq, gk)
+    want = ref.prefill(n, q, k, v)
+    m = metrics(got, want)
+    assert meets_bar(m), fmt(m)
+    kg, vg = L.readCache(n)
+    assert np.array_equal(kg, ref.kc[:n * HKV * D]) and np.array_equal(vg, ref.vc[:n * HKV * D])
+    assert L.nKeys == n
+
+
+def test_prefill_of_one_matches_decode_reference(rng):
+    # test_prefill.ts:60-75: N=1 prefill against the DECODE reference.
+    gq, gk = gains(rng)
+    q, k, v = inputs(rng, 1)
+    L = Layer.create(CFG, gq, gk)
+    L.encodePrefill(1, q, k, v)
+    want = RefLayer(gq, gk).decode(q, k, v)
+    m = metrics(L.readOutput(1), want)
+    assert meets_bar(m), fmt(m)
+
+
+@pytest.mark.parametrize("n", [2, 7, 13, 33])
+def test_prefill_equals_decode_steps(rng, n):
+    gq, gk = gains(rng)
+    q, k, v = inputs(rng, n)
+    A = Layer.create(CFG, gq, gk)
+    A.encodePrefill(n, q, k, v)
+    out_a = A.readOutput(n)
+    B = Layer.create(CFG, gq, gk)
+    out_b = []
+    for i in range(n):
+        B.encode(tok(q, i, H * D), tok(k, i, HKV * D), tok(v, i, HKV * D))
+        out_b.append(B.readOutput(1))
+    out_b = np.concatenate(out_b)
+    assert oracle.abs_err_scaled(out_a, out_b, oracle.amax(out_b)) < 2e-5
+    ka, va = A.readCache(n)
+    kb, vb = B.readCache(n)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb), "KV cache not bit-identical"
+    assert A.nKeys == n and B.nKeys == n
+
+
+def test_prefill_then_decode(rng):
+    # test_prefill.ts:140-186: a prompt prefill followed by decode steps equals
+    # the reference doing the same.
+    gq, gk = gains(rng)
+    L, ref = Layer.create(CFG, gq, gk), RefLayer(gq, gk)
+    q, k, v = inputs(rng, 20)
+    L.encodePrefill(20, q, k, v)
+    m = metrics(L.readOutput(20), ref.prefill(20, q, k, v))
+    assert meets_bar(m), fmt(m)
+    for _ in range(4):
+        q1, k1, v1 = inputs(rng, 1)
+        L.encode(q1, k1, v1)
+        m = metrics(L.readOutput(1), ref.decode(q1, k1, v1))
+        assert meets_bar(m), fmt(m)
+    assert L.nKeys == 24
+    kg, vg = L.readCache(24)
+    assert np.array_equal(kg, ref.kc[:24 * HKV * D]) and np.array_equal(vg, ref.vc[:24 * HKV * D])
+
+
+def test_rope_position_is_live(rng):
+    # test_prefill.ts:188-261: the same tokens at pos0 = 0 and pos0 = 900 give
+    # O(1)-different outputs, and identical tokens within one prefill differ.
+    gq, gk = gains(rng)
+    n = 6
+    q1, k1, v1 = inputs(rng, 1)
+    q, k, v = np.tile(q1, n), np.tile(k1, n), np.tile(v1, n)
+    A = Layer.create(CFG, gq, gk)
+    A.encodePrefill(n, q, k, v)
+    at0 = A.readOutput(n)
+    B = Layer.create(CFG, gq, gk)
+    for _ in range(5):
+        B.encodePrefill(180, *inputs(rng, 180))
+    B.encodePrefill(n, q, k, v)
+    at900 = B.readOutput(n)
+    # Attention outputs are averages of N(0,1) values, so "O(1)" here is a
+    # change comparable to the outputs' own magnitude.
+    assert np.max(np.abs(at0 - at900)) > 0.3 * oracle.amax(at0)
+    tok_delta = np.max(np.abs(at900[:H * D] - at900[(n - 1) * H * D:]))
+    assert tok_delta > 1e-3
+    qn = B.readQn(n).reshape(n, H * D)
+    assert np.max(np.abs(qn[0] - qn[-1])) > 1e-2  # token i rotated by pos0 + i
+
+
+def test_chunked_prefill_equals_whole(rng):
+    gq, gk = gains(rng)
+    q, k, v = inputs(rng, 10)
+    A = Layer.create(CFG, gq, gk)
+    A.encodePrefill(10, q, k, v)
+    out_a = A.readOutput(10)
+    B = Layer.create(CFG, gq, gk)
+    B.encodePrefill(5, q[:5 * H * D], k[:5 * HKV * D], v[:5 * HKV * D])
+    first = B.readOutput(5)
+    B.encodePrefill(5, q[5 * H * D:], k[5 * HKV * D:], v[5 * HKV * D:])
+    second = B.readOutput(5)
+    out_b = np.concatenate([first, second])
+    assert oracle.abs_err_scaled(out_a, out_b, oracle.amax(out_a)) < 2e-5
+    ka, va = A.readCache(10)
+    kb, vb = B.readCache(10)
+    assert np.array_equal(ka, kb) and np.array_equal(va, vb)
+
+
+def test_guard_rails(rng):
+    gq, gk = gains(rng)
+    L = Layer.create(LayerConfig(maxKeys=40, maxPrefill=32), gq, gk)
+    with pytest.raises(ValueError, match="exceeds maxPrefill"):
+        L.encodePrefill(33, *inputs(rng, 33))
+    with pytest.raises(ValueError, match="expected"):
+        L.encodePrefill(2, *inputs(rng, 1))
+    with pytest.raises(ValueError):
+        L.encodePrefill(0)
+    assert L.nKeys == 0
+    L.encodePrefill(32, *inputs(rng, 32))
+    with pytest.raises(CacheFullError):
+        L.encodePrefill(9, *inputs(rng, 9))
+    L.encodePrefill(8, *inputs(rng, 8))
+    with pytest.raises(CacheFullError, match="full at 40"):
+        L.encode(*inputs(rng, 1))
+    with pytest.raises(layer_mod.DesyncError):
+        L.encode(*inputs(rng, 1), offset=39)
+    assert L.nKeys == 40
+    L.reset()
+    L.encode(*inputs(rng, 1), offset=0)
+    assert L.nKeys == 1

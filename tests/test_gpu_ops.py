@@ -1,0 +1,343 @@
+"""Kernel-level parity on the GPU, through the C ABI, against the CPU oracle.
+
+Mirrors the reference's kernel suites: test_ops.ts (rmsnorm, rope, decode
+attention, GQA planted map) and test_head.ts:259-389 (prefill attention, last
+query vs decode, causality). Shapes and tolerances follow those files; inputs
+are seeded (uniform [-1, 1) like randVec for the reference's own cases, N(0, 1)
+for the long-context cases), and each case also reports the distance of both
+results from the float64 closed form.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+from oracle import closed_form as cf
+from conftest import rand_unit, randn
+from parity import argmax_rows, fmt, meets_bar, metrics, top2_margin
+
+pytestmark = pytest.mark.gpu
+
+ops = pytest.importorskip("flock_amd.ops")
+
+EPS = oracle.QWEN3_EPS
+
+
+def dev(a) -> "ops.DeviceBuffer":
+    return ops.DeviceBuffer.from_array(np.ascontiguousarray(a, np.float32))
+
+
+def empty(n: int) -> "ops.DeviceBuffer":
+    return ops.DeviceBuffer(max(n, 1) * 4)
+
+
+def get(b, n: int) -> np.ndarray:
+    ops.sync()
+    return b.download(n)
+
+
+# ------------------------------------------------------------------ rmsnorm --
+@pytest.mark.parametrize("n,n_vecs", [(1024, 1), (128, 16), (128, 8), (1024, 4), (300, 3)])
+def test_rmsnorm_bit_exact(rng, n, n_vecs):
+    # test_ops.ts:100-135 (there: rel < 3e-7; here the oracle's rounding is
+    # reproduced exactly, so the bar is bit equality).
+    x, g = rand_unit(rng, n * n_vecs), rand_unit(rng, n, 0.5)
+    o = empty(n * n_vecs)
+    ops.rmsnorm(dev(x), dev(g), o, n, n_vecs, EPS)
+    got = get(o, n * n_vecs)
+    want = oracle.rmsnorm(x, g, n, n_vecs, EPS)
+    assert np.array_equal(got, want), f"{np.sum(got != want)} differ, rel {oracle.rel_err(got, want)}"
+
+
+def test_rmsnorm_deterministic_and_zero(rng):
+    # test_ops.ts:137-181: 6 runs bit-identical; zero input gives exactly 0.
+    n, nv = 128, 16
+    x, g = dev(rand_unit(rng, n * nv)), dev(rand_unit(rng, n, 0.5))
+    runs = []
+    for _ in range(6):
+        o = empty(n * nv)
+        ops.rmsnorm(x, g, o, n, nv, EPS)
+        runs.append(get(o, n * nv))
+    assert all(np.array_equal(r, runs[0]) for r in runs)
+    o = empty(n)
+    ops.rmsnorm(dev(np.zeros(n, np.float32)), g, o, n, 1, EPS)
+    z = get(o, n)
+    assert np.all(z == 0)
+
+
+# --------------------------------------------------------------------- rope --
+@pytest.mark.parametrize("pairing", ["neox", "norm"])
+@pytest.mark.parametrize("n_tokens,n_heads,pos0", [(1, 16, 0), (1, 16, 137), (1, 8, 137),
+                                                   (7, 16, 0), (3, 8, 32768)])
+def test_rope_matches_oracle(rng, pairing, n_tokens, n_heads, pos0):
+    # test_ops.ts:189-227 (abs/scale < 4e-7); plus positions near 32k.
+    d = 128
+    inv = ops.rope_inv_freq(d, 1e6)
+    assert np.array_equal(inv, oracle.rope_inv_freq(d, 1e6))
+    x = rand_unit(rng, n_tokens * n_heads * d)
+    xb = dev(x)
+    ops.rope(xb, dev(inv), n_tokens, n_heads, d, pos0, pairing)
+    got = get(xb, x.size)
+    want = oracle.rope(x, n_tokens, n_heads, d, pos0, inv, pairing)
+    e = oracle.abs_err_scaled(got, want, oracle.amax(x))
+    assert e < 4e-7
+    assert np.sum(got != want) == 0, f"{np.sum(got != want)} of {x.size} not bit-identical"
+
+
+@pytest.mark.parametrize("pairing", ["neox", "norm"])
+def test_rope_planted_pair(pairing):
+    # test_ops.ts:229-263.
+    d = 128
+    inv = ops.rope_inv_freq(d, 1e6)
+    x = np.zeros(d, np.float32)
+    x[0] = 1
+    xb = dev(x)
+    ops.rope(xb, dev(inv), 1, 1, d, 1, pairing)
+    got = get(xb, d)
+    partner, other = (1, 64) if pairing == "norm" else (64, 1)
+    assert abs(got[0] - np.cos(inv[0])) < 1e-6 and abs(got[partner] - np.sin(inv[0])) < 1e-6
+    assert got[other] == 0
+
+
+# ----------------------------------------------------------------- prologue --
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("pairing", ["neox", "norm"])
+@pytest.mark.parametrize("n,pos0", [(1, 0), (5, 40), (33, 900), (2, 32767)])
+def test_prologue_bit_exact(rng, d, pairing, n, pos0):
+    # layer.ts:598-622 / 722-741 fused: qn and the appended cache rows equal the
+    # oracle's rmsnorm -> rope -> append bit for bit, and equal the unfused
+    # flk_rmsnorm + flk_rope + flk_kv_append path.
+    H, Hkv = 16, 8
+    maxk = pos0 + n + 3
+    q, k, v = randn(rng, n * H * d), randn(rng, n * Hkv * d), randn(rng, n * Hkv * d)
+    gq = rng.normal(1, 0.1, d).astype(np.float32)
+    gk = rng.normal(1, 0.1, d).astype(np.float32)
+    inv = ops.rope_inv_freq(d, 1e6)
+    kc, vc, qn = empty(maxk * Hkv * d), empty(maxk * Hkv * d), empty(n * H * d)
+    ops.qk_prologue(dev(q), dev(k), dev(v), dev(gq), dev(gk), dev(inv), EPS, pairing, qn, kc, vc,
+                    n, pos0, H, Hkv, d, maxk)
+    row = Hkv * d
+    got_q = get(qn, n * H * d)
+    got_k = kc.download(maxk * row)[pos0 * row:(pos0 + n) * row]
+    got_v = vc.download(maxk * row)[pos0 * row:(pos0 + n) * row]
+    want_q = oracle.rope(oracle.rmsnorm(q, gq, d, n * H, EPS), n, H, d, pos0, inv, pairing)
+    want_k = oracle.rope(oracle.rmsnorm(k, gk, d, n * Hkv, EPS), n, Hkv, d, pos0, inv, pairing)
+    assert np.array_equal(got_q, want_q), f"q: {np.sum(got_q != want_q)} differ"
+    assert np.array_equal(got_k, want_k), f"k: {np.sum(got_k != want_k)} differ"
+    assert np.array_equal(got_v, v)
+    # Unfused path.
+    qb, kb = empty(n * H * d), empty(n * Hkv * d)
+    ops.rmsnorm(dev(q), dev(gq), qb, d, n * H, EPS)
+    ops.rmsnorm(dev(k), dev(gk), kb, d, n * Hkv, EPS)
+    ops.rope(qb, dev(inv), n, H, d, pos0, pairing)
+    ops.rope(kb, dev(inv), n, Hkv, d, pos0, pairing)
+    kc2, vc2 = empty(maxk * Hkv * d), empty(maxk * Hkv * d)
+    ops.kv_append(kb, dev(v), kc2, vc2, n, pos0, Hkv, d, maxk)
+    assert np.array_equal(get(qb, n * H * d), got_q)
+    assert np.array_equal(kc2.download(maxk * row)[pos0 * row:(pos0 + n) * row], got_k)
+
+
+# ------------------------------------------------------------------- decode --
+def _decode(q, k, v, H, Hkv, d, nk):
+    ws = ops.Workspace(H, Hkv, d, nk)
+    o = empty(H * d)
+    ops.attn_decode(dev(q), dev(k), dev(v), o, H, Hkv, d, nk, ws)
+    return get(o, H * d)
+
+
+@pytest.mark.parametrize("H,Hkv,nk", [(16, 8, 1), (16, 8, 137), (16, 8, 512), (16, 16, 64),
+                                      (4, 1, 33)])
+def test_decode_reference_cases(rng, H, Hkv, nk):
+    # test_ops.ts:316-355: relErr(floor 1e-3) < 1e-4 on randVec inputs.
+    d = 128
+    q = rand_unit(rng, H * d)
+    k, v = rand_unit(rng, nk * Hkv * d), rand_unit(rng, nk * Hkv * d)
+    got = _decode(q, k, v, H, Hkv, d, nk)
+    want = oracle.attn(q, k, v, H, Hkv, d, nk)
+    m = metrics(got, want, cf.attention(q, k, v, H, Hkv, d, 1, nk - 1))
+    print(fmt(m))
+    assert m["rel"] < 1e-4 and m["max_abs"] < 2e-5
+    assert np.array_equal(argmax_rows(got, H), argmax_rows(want, H))
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("nk", [1, 2, 63, 64, 65, 513, 2049, 32769])
+def test_decode_north_star_bar(rng, d, nk):
+    # N(0,1) inputs (the long-context configs' distribution), split-K in play
+    # from a few hundred keys on.
+    H, Hkv = 16, 8
+    q = randn(rng, H * d)
+    k, v = randn(rng, nk * Hkv * d), randn(rng, nk * Hkv * d)
+    got = _decode(q, k, v, H, Hkv, d, nk)
+    want = oracle.attn(q, k, v, H, Hkv, d, nk)
+    m = metrics(got, want, cf.attention(q, k, v, H, Hkv, d, 1, nk - 1))
+    print(fmt(m))
+    assert meets_bar(m), fmt(m)
+    assert np.array_equal(argmax_rows(got, H), argmax_rows(want, H)), top2_margin(want, H)
+
+
+def test_decode_gqa_planted_kat():
+    # test_ops.ts:357-392: heads 0,1 read kv head 0 (all 7), heads 2,3 read kv
+    # head 1 (all -3), exactly.
+    d = 128
+    v = np.concatenate([np.full(d, 7, np.float32), np.full(d, -3, np.float32)])
+    got = _decode(np.zeros(4 * d, np.float32), np.zeros(2 * d, np.float32), v, 4, 2, d, 1)
+    got = got.reshape(4, d)
+    assert np.all(got[:2] == 7) and np.all(got[2:] == -3)
+
+
+def test_decode_deterministic_across_runs(rng):
+    # The race check of test_ops.ts:137-165 applied to split-K decode: the
+    # cross-split merge order is fixed, so repeated runs are bit-identical.
+    H, Hkv, d, nk = 16, 8, 128, 20000
+    q, k, v = dev(randn(rng, H * d)), dev(randn(rng, nk * Hkv * d)), dev(randn(rng, nk * Hkv * d))
+    ws = ops.Workspace(H, Hkv, d, nk)
+    outs = []
+    for _ in range(6):
+        o = empty(H * d)
+        ops.attn_decode(q, k, v, o, H, Hkv, d, nk, ws)
+        outs.append(get(o, H * d))
+    assert all(np.array_equal(x, outs[0]) for x in outs)
+
+
+def test_decode_layer_fused_matches_oracle(rng):
+    # Layer.encode's attention slice in one launch (layer.ts:571-630) vs the
+    # oracle's layerForwardRef slice (layer_ref.ts:46-70).
+    H, Hkv, d, pos = 16, 8, 128, 700
+    maxk = 1024
+    kc0, vc0 = randn(rng, maxk * Hkv * d), randn(rng, maxk * Hkv * d)
+    q, k, v = randn(rng, H * d), randn(rng, Hkv * d), randn(rng, Hkv * d)
+    gq = rng.normal(1, 0.1, d).astype(np.float32)
+    gk = rng.normal(1, 0.1, d).astype(np.float32)
+    inv = ops.rope_inv_freq(d, 1e6)
+    kc, vc = dev(kc0), dev(vc0)
+    qn, o = empty(H * d), empty(H * d)
+    ws = ops.Workspace(H, Hkv, d, maxk)
+    ops.decode_layer(dev(q), dev(k), dev(v), dev(gq), dev(gk), dev(inv), EPS, "neox", qn, kc, vc,
+                     o, pos, H, Hkv, d, maxk, ws)
+    got_o, got_qn = get(o, H * d), qn.download(H * d)
+    got_kc, got_vc = kc.download(maxk * Hkv * d), vc.download(maxk * Hkv * d)
+    kco, vco = kc0.copy(), vc0.copy()
+    want_qn, want_o = oracle.layer_attn_decode(q, k, v, gq, gk, inv, kco, vco, pos, H, Hkv, d)
+    assert np.array_equal(got_qn, want_qn)
+    assert np.array_equal(got_kc, kco) and np.array_equal(got_vc, vco)
+    m = metrics(got_o, want_o)
+    assert meets_bar(m), fmt(m)
+
+
+# ------------------------------------------------------------------ prefill --
+def _prefill(q, k, v, H, Hkv, d, nq, pos0):
+    ws = ops.Workspace(H, Hkv, d, pos0 + nq, nq)
+    o = empty(nq * H * d)
+    ops.attn_prefill(dev(q), dev(k), dev(v), o, H, Hkv, d, nq, pos0, ws)
+    return get(o, nq * H * d)
+
+
+PREFILL_CASES = [
+    # test_head.ts:290-304
+    (16, 8, 1, 0), (16, 8, 7, 0), (16, 8, 13, 0), (16, 8, 64, 0), (16, 8, 65, 0),
+    (16, 8, 129, 0), (16, 8, 5, 40), (16, 8, 20, 300), (16, 16, 9, 0), (4, 1, 11, 0),
+    (16, 8, 3, 2100),
+]
+
+
+@pytest.mark.parametrize("H,Hkv,nq,pos0", PREFILL_CASES)
+def test_prefill_reference_cases(rng, H, Hkv, nq, pos0):
+    # abs/scale < 1e-5 against attnPrefillRef (test_head.ts:306-318), and the
+    # north-star bar.
+    d = 128
+    nk = pos0 + nq
+    q = rand_unit(rng, nq * H * d)
+    k, v = rand_unit(rng, nk * Hkv * d), rand_unit(rng, nk * Hkv * d)
+    got = _prefill(q, k, v, H, Hkv, d, nq, pos0)
+    want = oracle.attn_prefill(q, k, v, H, Hkv, d, nq, pos0)
+    m = metrics(got, want, cf.attention(q, k, v, H, Hkv, d, nq, pos0))
+    print(fmt(m))
+    assert m["abs_scaled"] < 1e-5
+    assert meets_bar(m), fmt(m)
+    assert np.array_equal(argmax_rows(got, nq * H), argmax_rows(want, nq * H))
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("H,Hkv,nq,pos0", [(16, 8, 200, 0), (16, 8, 64, 4000), (12, 4, 50, 77),
+                                           (16, 2, 33, 10), (8, 8, 130, 3)])
+def test_prefill_split_and_shapes(rng, d, H, Hkv, nq, pos0):
+    # Long caches exercise the key-split + merge; odd groups exercise the
+    # row -> (query, head) map (group 3 leaves rows 126, 127 of a tile unused).
+    nk = pos0 + nq
+    q = randn(rng, nq * H * d)
+    k, v = randn(rng, nk * Hkv * d), randn(rng, nk * Hkv * d)
+    got = _prefill(q, k, v, H, Hkv, d, nq, pos0)
+    want = oracle.attn_prefill(q, k, v, H, Hkv, d, nq, pos0)
+    m = metrics(got, want, cf.attention(q, k, v, H, Hkv, d, nq, pos0))
+    print(fmt(m))
+    assert meets_bar(m), fmt(m)
+
+
+def test_prefill_queries_match_decode(rng):
+    # test_head.ts:321-351: prefill query `at` equals the decode reference over
+    # keys 0..at -- proves the causal bound is pos0 + qi + 1.
+    H, Hkv, d, nq = 16, 8, 128, 9
+    q = rand_unit(rng, nq * H * d)
+    k, v = rand_unit(rng, nq * Hkv * d), rand_unit(rng, nq * Hkv * d)
+    pre = _prefill(q, k, v, H, Hkv, d, nq, 0).reshape(nq, H * d)
+    for at in (0, 1, 4, nq - 1):
+        want = oracle.attn(q.reshape(nq, -1)[at], k[:(at + 1) * Hkv * d], v[:(at + 1) * Hkv * d],
+                           H, Hkv, d, at + 1)
+        assert oracle.abs_err_scaled(pre[at], want, oracle.amax(want)) < 2e-5
+
+
+def test_prefill_causality_bit_identical(rng):
+    # test_head.ts:353-389.
+    H, Hkv, d, nq = 16, 8, 128, 8
+    q = rand_unit(rng, nq * H * d)
+    k, v = rand_unit(rng, nq * Hkv * d), rand_unit(rng, nq * Hkv * d)
+    base = _prefill(q, k, v, H, Hkv, d, nq, 0).reshape(nq, -1)
+    k2, v2 = k.copy(), v.copy()
+    idx = np.arange(Hkv * d)
+    k2[5 * Hkv * d + idx] = 9 + idx * 0.01
+    v2[5 * Hkv * d + idx] = -7 - idx * 0.01
+    pert = _prefill(q, k2, v2, H, Hkv, d, nq, 0).reshape(nq, -1)
+    assert np.array_equal(base[:5], pert[:5])
+    assert np.sum(base[5:] != pert[5:]) > H * d
+
+
+def test_prefill_deterministic_across_runs(rng):
+    H, Hkv, d, nq, pos0 = 16, 8, 128, 64, 5000
+    nk = pos0 + nq
+    q, k, v = dev(randn(rng, nq * H * d)), dev(randn(rng, nk * Hkv * d)), dev(randn(rng, nk * Hkv * d))
+    ws = ops.Workspace(H, Hkv, d, nk, nq)
+    outs = []
+    for _ in range(6):
+        o = empty(nq * H * d)
+        ops.attn_prefill(q, k, v, o, H, Hkv, d, nq, pos0, ws)
+        outs.append(get(o, nq * H * d))
+    assert all(np.array_equal(x, outs[0]) for x in outs)
+
+
+# ------------------------------------------------------------------- ragged --
+def test_decode_ragged_matches_per_sequence_oracle(rng):
+    # Extension (no reference counterpart): independent sequences, one launch.
+    H, Hkv, d, B = 16, 8, 128, 9
+    lens = np.array([1, 5, 64, 65, 300, 1000, 2500, 0, 777], np.uint32)
+    offs = np.concatenate([[0], np.cumsum(lens + 3)[:-1]]).astype(np.uint64)  # gaps between seqs
+    rows = int(offs[-1] + lens[-1] + 3)
+    kc, vc = randn(rng, rows * Hkv * d), randn(rng, rows * Hkv * d)
+    q = randn(rng, B * H * d)
+    ws = ops.Workspace(H, Hkv, d, int(lens.max()), 0, B)
+    o = empty(B * H * d)
+    ops.attn_decode_ragged(dev(q), dev(kc), dev(vc), ops.DeviceBuffer.from_array(offs),
+                           ops.DeviceBuffer.from_array(lens), o, B, int(lens.max()), H, Hkv, d, ws)
+    got = get(o, B * H * d).reshape(B, H * d)
+    row = Hkv * d
+    for b in range(B):
+        if lens[b] == 0:
+            assert np.all(got[b] == 0)
+            continue
+        s = int(offs[b]) * row
+        qb = q[b * H * d:(b + 1) * H * d]
+        kb, vb = kc[s:s + int(lens[b]) * row], vc[s:s + int(lens[b]) * row]
+        want = oracle.attn(qb, kb, vb, H, Hkv, d, int(lens[b]))
+        m = metrics(got[b], want, cf.attention(qb, kb, vb, H, Hkv, d, 1, int(lens[b]) - 1))
+        assert meets_bar(m), (b, fmt(m))
