@@ -42,7 +42,6 @@ SIGNATURES: dict[str, tuple] = {
     "flk_sync": (_i32, []),
     "flk_workspace_bytes": (_u64, [_u32, _u32, _u32, _u32, _u32, _u32]),
     "flk_call_workspace_bytes": (_u64, [_i32, _u32, _u32, _u32, _u32, _u32, _u32]),
-    "flk_workspace_init": (_i32, [_p, _u64]),
     "flk_rmsnorm": (_i32, [_p, _p, _p, _u32, _u32, _f32]),
     "flk_rope": (_i32, [_p, _p, _u32, _u32, _u32, _u32, _i32]),
     "flk_kv_append": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32]),

@@ -24,7 +24,7 @@ HIPCC_FLAGS = [
     "-std=c++17",
     "-fPIC",
     "-shared",
-    "-ffp-contract=fast",
+    "-ffp-contract=off",  # rounding points are explicit (fmaf where wanted)
     # Keep hipcc from forming packed-f32 instructions (v_pk_*_f32).
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-Wall",

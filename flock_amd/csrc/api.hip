@@ -43,6 +43,7 @@ static int32_t check_heads(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_
 }
 
 static int32_t check_ws(void* ws, uint64_t ws_bytes, uint64_t need) {
+  if (need == 0) return FLK_OK;  // single-split launch: no partials
   if (ws == nullptr || ws_bytes < need)
     return fail(FLK_ERR_WORKSPACE, "workspace of %llu bytes needed, got %llu%s",
                 (unsigned long long)need, (unsigned long long)ws_bytes,
@@ -51,6 +52,19 @@ static int32_t check_ws(void* ws, uint64_t ws_bytes, uint64_t need) {
     return fail(FLK_ERR_WORKSPACE, "workspace must be 256-byte aligned");
   return FLK_OK;
 }
+
+// The attention kernels move 16-byte vectors (float4) of q, o and the caches.
+static int32_t check_vec4(const void* p, const char* name) {
+  if (reinterpret_cast<uintptr_t>(p) % 16 != 0)
+    return fail(FLK_ERR_ARG, "%s must be 16-byte aligned", name);
+  return FLK_OK;
+}
+
+#define FLK_ALIGNED(p)                                                  \
+  do {                                                                  \
+    int32_t rc_ = check_vec4((p), #p);                                  \
+    if (rc_) return rc_;                                                \
+  } while (0)
 
 #define FLK_NONNULL(p)                                                  \
   do {                                                                  \
@@ -139,7 +153,7 @@ uint64_t flk_workspace_bytes(uint32_t n_heads, uint32_t n_kv_heads, uint32_t hea
     const uint64_t b = prefill_ws_bound(n_heads, n_kv_heads, head_dim, nq, max_keys);
     if (b > need) need = b;
   }
-  return (need + 255) / 256 * 256;
+  return ws_align(need > 0 ? need : 1);
 }
 
 uint64_t flk_call_workspace_bytes(int32_t kind, uint32_t n_heads, uint32_t n_kv_heads,
@@ -156,12 +170,6 @@ uint64_t flk_call_workspace_bytes(int32_t kind, uint32_t n_heads, uint32_t n_kv_
     default:
       return 0;
   }
-}
-
-int32_t flk_workspace_init(void* ws, uint64_t ws_bytes) {
-  FLK_NONNULL(ws);
-  if (ws_bytes < kCounterBytes) return fail(FLK_ERR_WORKSPACE, "workspace smaller than counters");
-  return hip_status(hipMemsetAsync(ws, 0, kCounterBytes, g_stream), "flk_workspace_init");
 }
 
 int32_t flk_rmsnorm(const float* x, const float* g, float* o, uint32_t n, uint32_t n_vecs,
@@ -240,6 +248,10 @@ int32_t flk_attn_decode(const float* q, const float* kcache, const float* vcache
   FLK_NONNULL(kcache);
   FLK_NONNULL(vcache);
   FLK_NONNULL(o);
+  FLK_ALIGNED(q);
+  FLK_ALIGNED(kcache);
+  FLK_ALIGNED(vcache);
+  FLK_ALIGNED(o);
   int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
   if (rc) return rc;
   if (n_keys == 0) return fail(FLK_ERR_ARG, "decode n_keys must be >= 1");
@@ -257,6 +269,10 @@ int32_t flk_attn_prefill(const float* q, const float* kcache, const float* vcach
   FLK_NONNULL(kcache);
   FLK_NONNULL(vcache);
   FLK_NONNULL(o);
+  FLK_ALIGNED(q);
+  FLK_ALIGNED(kcache);
+  FLK_ALIGNED(vcache);
+  FLK_ALIGNED(o);
   int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
   if (rc) return rc;
   if (n_queries == 0) return fail(FLK_ERR_ARG, "prefill n_queries must be >= 1");
@@ -285,6 +301,10 @@ int32_t flk_decode_layer(const float* q_raw, const float* k_raw, const float* v_
   FLK_NONNULL(kcache);
   FLK_NONNULL(vcache);
   FLK_NONNULL(o);
+  FLK_ALIGNED(qn_out);
+  FLK_ALIGNED(kcache);
+  FLK_ALIGNED(vcache);
+  FLK_ALIGNED(o);
   int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
   if (rc) return rc;
   if (pairing != FLK_ROPE_NEOX && pairing != FLK_ROPE_NORM)
@@ -320,13 +340,16 @@ int32_t flk_attn_decode_ragged(const float* q, const float* kcache, const float*
   FLK_NONNULL(seq_row_off);
   FLK_NONNULL(n_keys);
   FLK_NONNULL(o);
+  FLK_ALIGNED(q);
+  FLK_ALIGNED(kcache);
+  FLK_ALIGNED(vcache);
+  FLK_ALIGNED(o);
   int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
   if (rc) return rc;
   if (n_seqs == 0 || max_n_keys == 0)
     return fail(FLK_ERR_ARG, "ragged decode n_seqs=%u max_n_keys=%u", n_seqs, max_n_keys);
-  if ((uint64_t)n_seqs * n_kv_heads > kMaxCounters)
-    return fail(FLK_ERR_UNSUPPORTED, "n_seqs * n_kv_heads exceeds %llu",
-                (unsigned long long)kMaxCounters);
+  if (n_seqs > 65535)
+    return fail(FLK_ERR_UNSUPPORTED, "ragged decode n_seqs %u exceeds 65535 (grid z)", n_seqs);
   const DecodeShape s{n_heads, n_kv_heads, head_dim, n_seqs, max_n_keys};
   rc = check_ws(ws, ws_bytes, decode_ws_bytes(s));
   if (rc) return rc;

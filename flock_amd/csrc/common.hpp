@@ -25,12 +25,32 @@ __device__ __forceinline__ float rsqrt_once(float y) { return (float)(1.0 / sqrt
 // ------------------------------------------------------------- lane shuffles --
 __device__ __forceinline__ float shfl_xor(float v, int mask) { return __shfl_xor(v, mask, kWave); }
 
-// Sum over aligned groups of `width` lanes (width a power of two <= 64); every
-// lane of the group ends with the group total.
+// Data-parallel-primitive move: lane i reads lane f(i) of v within its row of
+// 16 lanes (CTRL is the DPP control word). Runs as a VALU modifier, no LDS.
+template <int CTRL>
+__device__ __forceinline__ float dpp(float v) {
+  return __builtin_bit_cast(
+      float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, v), CTRL, 0xF, 0xF, false));
+}
+constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
+constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppHalfMirror = 0x141; // lane i <- 7 - i within 8
+constexpr int kDppMirror = 0x140;     // lane i <- 15 - i within 16
+
+// Sum over aligned groups of `width` lanes (a power of two <= 64); every lane
+// of a group ends with the same total (each step adds a pair of equal-shaped
+// partial sums, so both partners compute the same float). Must be called with
+// all lanes of the wave active.
 template <int width>
 __device__ __forceinline__ float group_sum(float v) {
-#pragma unroll
-  for (int m = 1; m < width; m <<= 1) v += shfl_xor(v, m);
+  static_assert(width >= 1 && width <= 64 && (width & (width - 1)) == 0, "width");
+  if (width >= 2) v += dpp<kDppXor1>(v);
+  if (width >= 4) v += dpp<kDppXor2>(v);
+  if (width >= 8) v += dpp<kDppHalfMirror>(v);
+  if (width >= 16) v += dpp<kDppMirror>(v);
+  if (width >= 32)  // swap the two 16-lane halves of each 32-lane group
+    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+  if (width >= 64) v += shfl_xor(v, 32);
   return v;
 }
 
@@ -160,9 +180,10 @@ hipError_t launch_prefill(const float* q, const float* kcache, const float* vcac
                           uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                           uint32_t n_queries, uint32_t pos0, void* ws, hipStream_t st);
 
-// Workspace layout: [counters: kCounterBytes][partials ...]. Counters are
-// uint32 and are returned to zero by the kernels that use them.
-constexpr uint64_t kCounterBytes = 64 * 1024;
-constexpr uint64_t kMaxCounters = kCounterBytes / 4;
+// Workspace layout (split-K partials): [(m, l) pairs][pad to 256 B][acc rows].
+constexpr uint64_t kWsAlign = 256;
+__host__ __device__ constexpr uint64_t ws_align(uint64_t n) {
+  return (n + kWsAlign - 1) / kWsAlign * kWsAlign;
+}
 
 }  // namespace flk

@@ -2,21 +2,23 @@
 //
 // The reference kernel (attention.wgsl:58-122) runs one 128-thread workgroup
 // per q-head and holds every score in workgroup memory, which caps context at
-// $MAX_KEYS and leaves the GPU with 16 workgroups. Here:
+// $MAX_KEYS and leaves the GPU with 16 workgroups. Here two launches:
 //
-//   grid  = (n_kv_heads, n_splits, n_seqs); block = 256 threads (4 waves)
+// decode_split_kernel  grid (n_kv_heads, n_splits, n_seqs), 256 threads.
 //   One workgroup streams keys [t0, t1) of one kv head and serves all G =
 //   n_heads / n_kv_heads query heads that read it, so each K/V byte is read
-//   from HBM once. Each 128-float K/V row is loaded by D/4 lanes as float4
-//   (one 512 B coalesced segment per row for D = 128); a workgroup has
-//   256 / (D/4) "slots" that take keys t = t0 + slot, t0 + slot + SLOTS, ...
-//   and U keys per slot are in flight per iteration.
-//   Scores: per-lane float4 dot + a lane-group sum; online softmax (running
-//   max m, denominator l, unnormalised accumulator acc) updated once per U keys.
-//   Slots merge through LDS. With one split the workgroup writes o directly;
-//   otherwise it writes (m, l, acc) to the workspace and the LAST workgroup of
-//   its (sequence, kv head) -- found with a device-scope atomic counter --
-//   merges every split with log-sum-exp weights and resets the counter.
+//   from HBM once. Each K/V row of one kv head (D floats) is loaded by D/4
+//   lanes as float4 -- one coalesced 512 B segment for D = 128 -- so a
+//   workgroup has 256 / (D/4) "slots", slot s taking keys t0 + s, t0 + s +
+//   SLOTS, ..., and U keys per slot are in flight per iteration.
+//   Scores: per-lane float4 dot, then a DPP/swizzle sum over the row's lanes;
+//   online softmax (running max m, denominator l, unnormalised accumulator)
+//   per slot; the slots merge through LDS. A single-split row writes o
+//   directly, otherwise the workgroup writes its (m, l, acc) partial.
+// decode_merge_kernel  grid (n_heads, n_seqs), 256 threads: combines the
+//   partials of one head with log-sum-exp weights (rows of a single split exit).
+// The two launches are ordered by the stream: no atomics or device-scope fences
+// inside a launch.
 //
 // Fused mode (flk_decode_layer) prepends Layer.encode's prologue
 // (layer.ts:598-622): every workgroup recomputes q's per-head RMSNorm + RoPE
@@ -36,12 +38,11 @@ struct DecodeArgs {
   float* o;
   const uint64_t* seq_row_off;  // ragged only
   const uint32_t* n_keys_dev;   // ragged only
-  uint32_t n_keys;              // single sequence
+  uint32_t n_keys;              // single sequence (ragged: the bound max_n_keys)
   uint32_t n_heads, n_kv_heads;
   uint32_t kps;                 // keys per split
   uint32_t max_splits;
   float scale;
-  uint32_t* counters;
   float2* part_ml;              // [seq][head][split] (m, l)
   float* part_acc;              // [seq][head][split][D]
   // fused prologue (q_raw != nullptr)
@@ -58,22 +59,35 @@ struct DecodeArgs {
   float* vcache_w;
 };
 
+// Launch-shape tunables (compile-time; the defaults are the measured choice).
+#ifndef FLK_DECODE_UNROLL
+#define FLK_DECODE_UNROLL 8
+#endif
+#ifndef FLK_DECODE_TARGET_WG
+#define FLK_DECODE_TARGET_WG 1024
+#endif
 constexpr int kDecodeThreads = 256;
-constexpr int kDecodeUnroll = 8;
+constexpr int kDecodeUnroll = FLK_DECODE_UNROLL;
+constexpr int kMergeThreads = 256;
+
+// Keys sequence `seq` attends: the argument for one sequence; for a ragged
+// batch its n_keys entry, clamped to the planned bound so that the grid covers
+// every split (n_keys == 0 marks an empty sequence).
+__device__ __forceinline__ uint32_t seq_keys(const DecodeArgs& a, uint32_t seq) {
+  return a.n_keys_dev != nullptr ? min(a.n_keys_dev[seq], a.n_keys) : a.n_keys;
+}
 
 template <int D, int G>
-__global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeArgs a) {
+__global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs a) {
   constexpr int LPK = D / 4;                    // lanes per key row
   constexpr int SLOTS = kDecodeThreads / LPK;   // concurrent keys per workgroup
   constexpr int U = kDecodeUnroll;
   constexpr int NT = G * LPK;                   // (head, float4 column) items
-  constexpr int GROUPS = NT >= kDecodeThreads ? 1 : kDecodeThreads / NT;
 
   __shared__ float4 s_q[G][LPK];
   __shared__ float s_m[SLOTS][G];
   __shared__ float s_l[SLOTS][G];
   __shared__ float4 s_acc[SLOTS][G][LPK];
-  __shared__ uint32_t s_last;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -83,29 +97,21 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeArgs a) {
   const uint32_t kvh = blockIdx.x;
   const uint32_t split = blockIdx.y;
   const uint32_t seq = blockIdx.z;
+  const uint32_t h0 = kvh * G;  // first q head of this group
 
-  uint32_t n_keys = a.n_keys;
-  uint64_t row0 = 0;
-  if (a.n_keys_dev != nullptr) {
-    // Ragged: the grid has max_splits splits, planned from a.n_keys (the
-    // caller's max_n_keys); a longer sequence is clamped to it so that every
-    // split of every sequence is launched and its counter returns to zero. An
-    // empty sequence gets a zero output row.
-    n_keys = min(a.n_keys_dev[seq], a.n_keys);
-    row0 = a.seq_row_off[seq];
-    if (n_keys == 0) {
-      if (split == 0)
-        for (int i = threadIdx.x; i < G * D; i += kDecodeThreads)
-          a.o[((size_t)seq * a.n_heads + kvh * G) * D + i] = 0.f;
-      return;
-    }
+  const uint32_t n_keys = seq_keys(a, seq);
+  const uint64_t row0 = a.seq_row_off != nullptr ? a.seq_row_off[seq] : 0;
+  if (n_keys == 0) {  // empty ragged sequence: zero output rows
+    if (split == 0)
+      for (int i = tid; i < G * D; i += kDecodeThreads)
+        a.o[((size_t)seq * a.n_heads + h0) * D + i] = 0.f;
+    return;
   }
   const uint32_t n_splits = (n_keys + a.kps - 1) / a.kps;
   if (split >= n_splits) return;  // uniform per workgroup
   const uint32_t t0 = split * a.kps;
   const uint32_t t1 = min(t0 + a.kps, n_keys);
   const size_t row = (size_t)a.n_kv_heads * D;  // floats per cache row
-  const uint32_t h0 = kvh * G;                  // first q head of this group
 
   // ---- q for the G heads (fused: prologue computed here) -------------------
   if (a.q_raw != nullptr) {
@@ -234,7 +240,6 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeArgs a) {
   for (int g = 0; g < G; g++) s_acc[slot][g][sl] = acc[g];
   __syncthreads();
 
-  const size_t part_head0 = ((size_t)seq * a.n_heads + h0) * a.max_splits;
   for (int i = tid; i < NT; i += kDecodeThreads) {
     const int g = i / LPK, c = i % LPK;
     float M = -INFINITY;
@@ -252,87 +257,81 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_kernel(DecodeArgs a) {
       A.w = fmaf(as.w, w, A.w);
     }
     if (n_splits == 1) {
-      float4 r = make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
+      const float4 r = make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
       reinterpret_cast<float4*>(a.o + ((size_t)seq * a.n_heads + h0 + g) * D)[c] = r;
     } else {
-      const size_t p = part_head0 + (size_t)g * a.max_splits + split;
+      const size_t p = ((size_t)seq * a.n_heads + h0 + g) * a.max_splits + split;
       if (c == 0) a.part_ml[p] = make_float2(M, L);
       reinterpret_cast<float4*>(a.part_acc + p * D)[c] = A;
     }
   }
-  if (n_splits == 1) return;
+}
 
-  // ---- cross-split merge by the last workgroup of (seq, kv head) -----------
-  __threadfence();
-  __syncthreads();
-  uint32_t* counter = a.counters + (size_t)seq * a.n_kv_heads + kvh;
-  if (tid == 0) s_last = atomicAdd(counter, 1u) == n_splits - 1 ? 1u : 0u;
-  __syncthreads();
-  if (s_last == 0) return;
-  __threadfence();
-  if (tid == 0) atomicExch(counter, 0u);
+// One workgroup per (head, sequence). Thread -> (group, float4 column): group
+// r folds splits r, r + GROUPS, ... with weights exp(m_s - M) against the
+// global max M; the groups then add up through LDS in a fixed order, so the
+// result does not depend on scheduling.
+template <int D>
+__global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs a) {
+  constexpr int LPK = D / 4;
+  constexpr int GROUPS = kMergeThreads / LPK;
+  __shared__ float s_max[GROUPS];
+  __shared__ float s_l[GROUPS];
+  __shared__ float4 s_acc[GROUPS][LPK];
 
-  // thread -> (group, g, c): each group folds every GROUPS-th split online,
-  // then the groups combine through LDS (reusing s_m / s_l / s_acc).
-  const int item = tid % NT;
-  const int grp = tid / NT;
-  const int g = item / LPK, c = item % LPK;
-  float M = -INFINITY, L = 0.f;
+  const uint32_t head = blockIdx.x;
+  const uint32_t seq = blockIdx.y;
+  const uint32_t n_keys = seq_keys(a, seq);
+  const uint32_t n_splits = (n_keys + a.kps - 1) / a.kps;
+  if (n_splits <= 1) return;  // written by the split kernel (or empty)
+  const int tid = threadIdx.x;
+  const int grp = tid / LPK, c = tid % LPK;
+  const size_t p0 = ((size_t)seq * a.n_heads + head) * a.max_splits;
+
+  float M = -INFINITY;
+  for (uint32_t s = grp; s < n_splits; s += GROUPS) M = fmaxf(M, a.part_ml[p0 + s].x);
+  if (c == 0) s_max[grp] = M;
+  __syncthreads();
+  M = s_max[0];
+#pragma unroll
+  for (int r = 1; r < GROUPS; r++) M = fmaxf(M, s_max[r]);
+
+  float L = 0.f;
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-  if (grp < GROUPS) {
-    for (uint32_t s = grp; s < n_splits; s += GROUPS) {
-      const size_t p = part_head0 + (size_t)g * a.max_splits + s;
-      const float2 ml = a.part_ml[p];
-      const float4 as = reinterpret_cast<const float4*>(a.part_acc + p * D)[c];
-      const float mn = fmaxf(M, ml.x);
-      const float w_old = M == -INFINITY ? 0.f : expf(M - mn);
-      const float w_new = expf(ml.x - mn);
-      L = L * w_old + ml.y * w_new;
-      A.x = A.x * w_old + as.x * w_new;
-      A.y = A.y * w_old + as.y * w_new;
-      A.z = A.z * w_old + as.z * w_new;
-      A.w = A.w * w_old + as.w * w_new;
-      M = mn;
-    }
+  for (uint32_t s = grp; s < n_splits; s += GROUPS) {
+    const float2 ml = a.part_ml[p0 + s];
+    const float w = ml.x == -INFINITY ? 0.f : expf(ml.x - M);
+    const float4 p = reinterpret_cast<const float4*>(a.part_acc + (p0 + s) * D)[c];
+    L = fmaf(ml.y, w, L);
+    A.x = fmaf(p.x, w, A.x);
+    A.y = fmaf(p.y, w, A.y);
+    A.z = fmaf(p.z, w, A.z);
+    A.w = fmaf(p.w, w, A.w);
   }
-  __syncthreads();  // everyone is done reading s_* from the slot merge
-  if (GROUPS > 1) {
-    if (grp < GROUPS) {
-      if (c == 0) {
-        s_m[grp][g] = M;
-        s_l[grp][g] = L;
-      }
-      s_acc[grp][g][c] = A;
-    }
-    __syncthreads();
-    if (grp == 0) {
-      float MM = -INFINITY;
-      for (int r = 0; r < GROUPS; r++) MM = fmaxf(MM, s_m[r][g]);
-      L = 0.f;
-      A = make_float4(0.f, 0.f, 0.f, 0.f);
-      for (int r = 0; r < GROUPS; r++) {
-        const float mr = s_m[r][g];
-        const float w = mr == -INFINITY ? 0.f : expf(mr - MM);
-        L = fmaf(s_l[r][g], w, L);
-        const float4 ar = s_acc[r][g][c];
-        A.x = fmaf(ar.x, w, A.x);
-        A.y = fmaf(ar.y, w, A.y);
-        A.z = fmaf(ar.z, w, A.z);
-        A.w = fmaf(ar.w, w, A.w);
-      }
-    }
+  if (c == 0) s_l[grp] = L;
+  s_acc[grp][c] = A;
+  __syncthreads();
+  if (grp != 0) return;
+  L = s_l[0];
+  A = s_acc[0][c];
+#pragma unroll
+  for (int r = 1; r < GROUPS; r++) {
+    L += s_l[r];
+    const float4 p = s_acc[r][c];
+    A.x += p.x;
+    A.y += p.y;
+    A.z += p.z;
+    A.w += p.w;
   }
-  if (grp == 0) {
-    float4 r = make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
-    reinterpret_cast<float4*>(a.o + ((size_t)seq * a.n_heads + h0 + g) * D)[c] = r;
-  }
+  reinterpret_cast<float4*>(a.o + ((size_t)seq * a.n_heads + head) * D)[c] =
+      make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
 }
 
 // ------------------------------------------------------------------ plan ----
-// Keys per split: aim for ~kTargetWG workgroups in total (several per CU so
-// that enough 512 B rows are in flight to cover HBM latency) while keeping
-// the per-kv-head merge small; multiples of SLOTS * U keys.
-constexpr uint32_t kTargetWG = 1024;
+// Keys per split: aim for ~kTargetWG split workgroups in total (several per CU
+// so that enough 512 B rows are in flight to cover HBM latency), in multiples
+// of one loop iteration (SLOTS * U keys), and at least kMinKps keys.
+constexpr uint32_t kTargetWG = FLK_DECODE_TARGET_WG;
 constexpr uint32_t kMinKps = 128;
 
 uint32_t decode_keys_per_split(const DecodeShape& s) {
@@ -349,17 +348,21 @@ static uint32_t max_splits_for(const DecodeShape& s) {
   return (s.max_n_keys + kps - 1) / kps;
 }
 
-static uint64_t ws_for_splits(const DecodeShape& s, uint64_t splits) {
-  const uint64_t slots = (uint64_t)s.n_seqs * s.n_heads * splits;
-  return kCounterBytes + slots * sizeof(float2) + slots * s.head_dim * sizeof(float) + 256;
+// Partials of `slots` (sequence, head, split) triples.
+static uint64_t ws_for_slots(uint64_t slots, uint32_t head_dim) {
+  return ws_align(slots * sizeof(float2)) + slots * head_dim * sizeof(float);
 }
 
-uint64_t decode_ws_bytes(const DecodeShape& s) { return ws_for_splits(s, max_splits_for(s)); }
+uint64_t decode_ws_bytes(const DecodeShape& s) {
+  const uint32_t splits = max_splits_for(s);
+  if (splits <= 1) return 0;
+  return ws_for_slots((uint64_t)s.n_seqs * s.n_heads * splits, s.head_dim);
+}
 
 // Bound over every call with n_keys <= s.max_n_keys and n_seqs <= s.n_seqs:
-// kps >= kMinKps and kps >= n_keys * n_kv_heads * n_seqs / kTargetWG, so a call
-// with n seqs has at most min(ceil(max / kMinKps), ceil(kTargetWG / (n_kv_heads
-// * n))) splits per sequence; take the largest n * splits over n.
+// kps >= kMinKps and kps >= n_keys * n_kv_heads * n / kTargetWG for a call
+// with n sequences, so it has at most min(ceil(max / kMinKps), ceil(kTargetWG
+// / (n_kv_heads * n))) splits per sequence; take the largest n * splits.
 uint64_t decode_ws_bound(const DecodeShape& s) {
   const uint64_t by_len = (s.max_n_keys + kMinKps - 1) / kMinKps;
   uint64_t best = 0;
@@ -369,17 +372,15 @@ uint64_t decode_ws_bound(const DecodeShape& s) {
     const uint64_t slots = n * (by_len < by_wg ? by_len : by_wg);
     if (slots > best) best = slots;
   }
-  DecodeShape one = s;
-  one.n_seqs = 1;
-  return ws_for_splits(one, best);
+  return ws_for_slots(best * s.n_heads, s.head_dim);
 }
 
 template <int D>
-static hipError_t launch_decode_d(const DecodeArgs& a, dim3 grid, uint32_t G, hipStream_t st) {
+static hipError_t launch_split_d(const DecodeArgs& a, dim3 grid, uint32_t G, hipStream_t st) {
   switch (G) {
-#define FLK_CASE(g)                                                                   \
-  case g:                                                                             \
-    hipLaunchKernelGGL((decode_kernel<D, g>), grid, dim3(kDecodeThreads), 0, st, a); \
+#define FLK_CASE(g)                                                                         \
+  case g:                                                                                   \
+    hipLaunchKernelGGL((decode_split_kernel<D, g>), grid, dim3(kDecodeThreads), 0, st, a); \
     break;
     FLK_CASE(1)
     FLK_CASE(2)
@@ -413,13 +414,12 @@ hipError_t launch_decode(const float* q, const float* kcache, const float* vcach
   a.kps = decode_keys_per_split(s);
   a.max_splits = max_splits_for(s);
   a.scale = (float)(1.0 / sqrt((double)s.head_dim));
-  char* w = static_cast<char*>(ws);
-  a.counters = reinterpret_cast<uint32_t*>(w);
-  const uint64_t slots = (uint64_t)s.n_seqs * s.n_heads * a.max_splits;
-  a.part_ml = reinterpret_cast<float2*>(w + kCounterBytes);
-  uint64_t acc_off = kCounterBytes + slots * sizeof(float2);
-  acc_off = (acc_off + 255) / 256 * 256;
-  a.part_acc = reinterpret_cast<float*>(w + acc_off);
+  if (a.max_splits > 1) {
+    char* w = static_cast<char*>(ws);
+    const uint64_t slots = (uint64_t)s.n_seqs * s.n_heads * a.max_splits;
+    a.part_ml = reinterpret_cast<float2*>(w);
+    a.part_acc = reinterpret_cast<float*>(w + ws_align(slots * sizeof(float2)));
+  }
   if (fused != nullptr) {
     a.q_raw = fused->q_raw;
     a.k_raw = fused->k_raw;
@@ -435,8 +435,15 @@ hipError_t launch_decode(const float* q, const float* kcache, const float* vcach
   }
   const dim3 grid(s.n_kv_heads, a.max_splits, s.n_seqs);
   const uint32_t G = s.n_heads / s.n_kv_heads;
-  if (s.head_dim == 128) return launch_decode_d<128>(a, grid, G, st);
-  return launch_decode_d<64>(a, grid, G, st);
+  hipError_t e = s.head_dim == 128 ? launch_split_d<128>(a, grid, G, st)
+                                   : launch_split_d<64>(a, grid, G, st);
+  if (e != hipSuccess || a.max_splits <= 1) return e;
+  const dim3 mgrid(s.n_heads, s.n_seqs);
+  if (s.head_dim == 128)
+    hipLaunchKernelGGL(decode_merge_kernel<128>, mgrid, dim3(kMergeThreads), 0, st, a);
+  else
+    hipLaunchKernelGGL(decode_merge_kernel<64>, mgrid, dim3(kMergeThreads), 0, st, a);
+  return hipGetLastError();
 }
 
 }  // namespace flk

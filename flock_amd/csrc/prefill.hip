@@ -341,7 +341,9 @@ uint64_t prefill_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_d
 }
 
 uint64_t prefill_ws_bytes(const PrefillPlan& p, uint32_t head_dim) {
-  return kCounterBytes + p.partial_slots * kRows * (sizeof(float2) + head_dim * sizeof(float)) + 256;
+  if (p.partial_slots == 0) return 0;
+  return ws_align(p.partial_slots * kRows * sizeof(float2)) +
+         p.partial_slots * kRows * head_dim * sizeof(float);
 }
 
 template <int D>
@@ -366,10 +368,10 @@ hipError_t launch_prefill(const float* q, const float* kcache, const float* vcac
   a.vcache = vcache;
   a.o = o;
   char* w = static_cast<char*>(ws);
-  a.part_ml = reinterpret_cast<float2*>(w + kCounterBytes);
-  uint64_t acc_off = kCounterBytes + p.partial_slots * kRows * sizeof(float2);
-  acc_off = (acc_off + 255) / 256 * 256;
-  a.part_acc = reinterpret_cast<float*>(w + acc_off);
+  if (p.partial_slots > 0) {
+    a.part_ml = reinterpret_cast<float2*>(w);
+    a.part_acc = reinterpret_cast<float*>(w + ws_align(p.partial_slots * kRows * sizeof(float2)));
+  }
   a.n_heads = n_heads;
   a.n_kv_heads = n_kv_heads;
   a.group = n_heads / n_kv_heads;

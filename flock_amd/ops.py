@@ -97,13 +97,12 @@ def workspace_bytes(n_heads: int, n_kv_heads: int, head_dim: int, max_keys: int,
 
 
 class Workspace(DeviceBuffer):
-    """Split-K scratch: sized by flk_workspace_bytes, counters zeroed once."""
+    """Split-K scratch sized by flk_workspace_bytes (no initialisation needed)."""
 
     def __init__(self, n_heads: int, n_kv_heads: int, head_dim: int, max_keys: int,
                  max_queries: int = 0, max_seqs: int = 1):
         super().__init__(workspace_bytes(n_heads, n_kv_heads, head_dim, max_keys, max_queries,
                                          max_seqs))
-        check(lib().flk_workspace_init(self.ptr, self.nbytes), "flk_workspace_init")
 
 
 def set_stream(stream) -> None:

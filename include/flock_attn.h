@@ -26,10 +26,10 @@
  *   - Launches are asynchronous and ordered on the library's current stream
  *     (flk_set_stream; default: the null stream). flk_sync() waits for it.
  *   - Split-K kernels need scratch for per-split partial results. The caller
- *     passes it as (ws, ws_bytes); size it with flk_workspace_bytes and zero it
- *     once with flk_workspace_init. Kernels leave its counters at zero on exit,
- *     so a workspace is reusable without re-clearing. Calls that share one
- *     workspace must be ordered on one stream (concurrent calls race).
+ *     passes it as (ws, ws_bytes), sized with flk_workspace_bytes; it needs no
+ *     initialisation and holds nothing between calls. Calls that share one
+ *     workspace must be ordered on one stream (concurrent calls race). A call
+ *     whose plan has a single split needs none (ws may then be NULL).
  *   - head_dim must be 64 or 128; n_heads must be a multiple of n_kv_heads
  *     with n_heads / n_kv_heads <= 8.
  */
@@ -83,12 +83,11 @@ uint64_t flk_workspace_bytes(uint32_t n_heads, uint32_t n_kv_heads, uint32_t hea
                              uint32_t max_keys, uint32_t max_queries, uint32_t max_seqs);
 /* Bytes one call needs. kind: FLK_CALL_DECODE (flk_attn_decode /
  * flk_decode_layer; n = n_keys), FLK_CALL_PREFILL (n = n_queries, pos0),
- * FLK_CALL_RAGGED (n = max_n_keys, n_seqs). 0 for an invalid shape. */
+ * FLK_CALL_RAGGED (n = max_n_keys, n_seqs). 0 when the call needs no workspace
+ * (a single-split plan) or the shape is invalid. */
 enum { FLK_CALL_DECODE = 0, FLK_CALL_PREFILL = 1, FLK_CALL_RAGGED = 2 };
 uint64_t flk_call_workspace_bytes(int32_t kind, uint32_t n_heads, uint32_t n_kv_heads,
                                   uint32_t head_dim, uint32_t n, uint32_t pos0, uint32_t n_seqs);
-/* Zero the workspace (once after allocation). */
-int32_t flk_workspace_init(void* ws, uint64_t ws_bytes);
 
 /* -------------------------------------------------------------- unfused ops -- */
 

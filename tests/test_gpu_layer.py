@@ -17,12 +17,13 @@ import numpy as np
 import pytest
 
 import oracle
+from oracle import closed_form as cf
 from conftest import randn
 from parity import fmt, meets_bar, metrics
 
 pytestmark = pytest.mark.gpu
 
-layer_mod = pytest.importorskip("flock_amd.layer")
+import flock_amd.layer as layer_mod  # noqa: E402
 Layer, LayerConfig = layer_mod.Layer, layer_mod.LayerConfig
 from flock_amd import CacheFullError  # noqa: E402
 
@@ -53,14 +54,16 @@ class RefLayer:
         self.n = 0
 
     def prefill(self, n, q, k, v):
-        _, o = oracle.layer_attn_prefill(q, k, v, self.gq, self.gk, self.inv, self.kc, self.vc,
-                                         n, self.n, H, HKV, D)
+        qn, o = oracle.layer_attn_prefill(q, k, v, self.gq, self.gk, self.inv, self.kc, self.vc,
+                                          n, self.n, H, HKV, D)
+        self.exact = cf.attention(qn, self.kc, self.vc, H, HKV, D, n, self.n)
         self.n += n
         return o
 
     def decode(self, q, k, v):
-        _, o = oracle.layer_attn_decode(q, k, v, self.gq, self.gk, self.inv, self.kc, self.vc,
-                                        self.n, H, HKV, D)
+        qn, o = oracle.layer_attn_decode(q, k, v, self.gq, self.gk, self.inv, self.kc, self.vc,
+                                         self.n, H, HKV, D)
+        self.exact = cf.attention(qn, self.kc, self.vc, H, HKV, D, 1, self.n)
         self.n += 1
         return o
 
@@ -74,7 +77,7 @@ def test_prefill_vs_cpu_reference(rng, n):
     got = L.readOutput(n)
     ref = RefLayer(gq, gk)
     want = ref.prefill(n, q, k, v)
-    m = metrics(got, want)
+    m = metrics(got, want, ref.exact)
     assert meets_bar(m), fmt(m)
     kg, vg = L.readCache(n)
     assert np.array_equal(kg, ref.kc[:n * HKV * D]) and np.array_equal(vg, ref.vc[:n * HKV * D])
@@ -87,8 +90,9 @@ def test_prefill_of_one_matches_decode_reference(rng):
     q, k, v = inputs(rng, 1)
     L = Layer.create(CFG, gq, gk)
     L.encodePrefill(1, q, k, v)
-    want = RefLayer(gq, gk).decode(q, k, v)
-    m = metrics(L.readOutput(1), want)
+    ref = RefLayer(gq, gk)
+    want = ref.decode(q, k, v)
+    m = metrics(L.readOutput(1), want, ref.exact)
     assert meets_bar(m), fmt(m)
 
 
@@ -119,12 +123,14 @@ def test_prefill_then_decode(rng):
     L, ref = Layer.create(CFG, gq, gk), RefLayer(gq, gk)
     q, k, v = inputs(rng, 20)
     L.encodePrefill(20, q, k, v)
-    m = metrics(L.readOutput(20), ref.prefill(20, q, k, v))
+    want = ref.prefill(20, q, k, v)
+    m = metrics(L.readOutput(20), want, ref.exact)
     assert meets_bar(m), fmt(m)
     for _ in range(4):
         q1, k1, v1 = inputs(rng, 1)
         L.encode(q1, k1, v1)
-        m = metrics(L.readOutput(1), ref.decode(q1, k1, v1))
+        want = ref.decode(q1, k1, v1)
+        m = metrics(L.readOutput(1), want, ref.exact)
         assert meets_bar(m), fmt(m)
     assert L.nKeys == 24
     kg, vg = L.readCache(24)

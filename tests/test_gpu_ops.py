@@ -19,7 +19,7 @@ from parity import argmax_rows, fmt, meets_bar, metrics, top2_margin
 
 pytestmark = pytest.mark.gpu
 
-ops = pytest.importorskip("flock_amd.ops")
+from flock_amd import ops  # noqa: E402  (no skip: a missing library must fail)
 
 EPS = oracle.QWEN3_EPS
 
