@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "../../include/flock_attn.h"
+#include "trig.hpp"
 
 namespace flk {
 
@@ -56,15 +57,14 @@ __device__ __forceinline__ float group_sum(float v) {
 
 // --------------------------------------------------------- RoPE + RMSNorm ----
 // One wave owns one head vector of D (64 or 128) floats: lane l holds element
-// l and, for D = 128, element l + 64. The sum of squares follows the reference
+// l and, for D = 128, element l + 64; g0, g1 are the gains of those elements. The sum of squares follows the reference
 // kernel's order exactly (rmsnorm.wgsl:45-66, rmsnormRef ops_ref.ts:20-49 with
 // wg = 128): partial[t] = x_t^2 (one element per partial), then a pairwise
 // tree with strides 64, 32, ..., 1. Stride 64 is in-lane; the rest is an xor
 // butterfly, after which every lane holds the tree total (each level's value
 // in lane i equals tree[i mod stride], and addition is commutative).
 template <int D>
-__device__ __forceinline__ void head_rmsnorm(float& e0, float& e1, const float* __restrict__ g,
-                                             int lane, float eps) {
+__device__ __forceinline__ void head_rmsnorm(float& e0, float& e1, float g0, float g1, float eps) {
   float p = e0 * e0;
   if (D == 128) p = p + e1 * e1;
 #pragma unroll
@@ -73,45 +73,54 @@ __device__ __forceinline__ void head_rmsnorm(float& e0, float& e1, const float* 
   // 1/sqrt as one rounding (ops_ref.ts:39-45).
   const float mean = p / (float)D;
   const float scale = rsqrt_once(mean + eps);
-  if (lane < D) e0 = (e0 * scale) * g[lane];
-  if (D == 128) e1 = (e1 * scale) * g[lane + 64];
+  e0 = (e0 * scale) * g0;
+  if (D == 128) e1 = (e1 * scale) * g1;
+}
+
+// cos/sin of RoPE angle theta = fr(pos * inv_freq[j]) (ops_ref.ts:75-76): the
+// product of an f32 and an integer position is formed exactly in f64 and
+// rounded once, and cos/sin are rounded once to f32 like fr(Math.cos(theta)).
+__device__ __forceinline__ float2 rope_cos_sin(float inv_f, uint32_t pos) {
+  const float theta = (float)((double)pos * (double)inv_f);
+  float s, c;
+  sincos_f32_exact(theta, s, c);
+  return make_float2(c, s);
 }
 
 // One rotated element: `x` is this element, `y` its pair partner, `first`
-// says whether this element is the pair's a (else b). theta = fr(pos *
-// inv_freq[j]); cos/sin in f64 rounded once, like the oracle's
-// fr(Math.cos(theta)); a' = fr(-b*s + fr(a*c)) and b' = fr(b*c + fr(a*s)) with
-// the f64 sum rounding before the f32 one (ops_ref.ts:80-88).
-__device__ __forceinline__ float rope_elem(float x, float y, bool first, float inv_f, int pos) {
-  const float theta = (float)pos * inv_f;
-  const float c = (float)cos((double)theta);
-  const float s = (float)sin((double)theta);
-  if (first) return (float)(-(double)y * (double)s + (double)(x * c));
-  return (float)((double)x * (double)c + (double)(y * s));
+// says whether this element is the pair's a (else b); cs = (cos, sin).
+// a' = fr(-b*s + fr(a*c)) and b' = fr(b*c + fr(a*s)), the f64 sum rounding
+// before the f32 one (ops_ref.ts:80-88).
+__device__ __forceinline__ float rope_rot(float x, float y, bool first, float2 cs) {
+  if (first) return (float)(-(double)y * (double)cs.y + (double)(x * cs.x));
+  return (float)((double)x * (double)cs.x + (double)(y * cs.y));
 }
 
-// RoPE on one head vector held as above, at absolute position `pos`
-// (rope.wgsl:50-78, ropeRef ops_ref.ts:65-92). NEOX pairs (j, j + D/2): for
-// D = 128 both halves sit in the same lane; for D = 64 the partner is lane
-// l ^ 32. NORM pairs (2j, 2j+1): the partner is lane l ^ 1.
+// RoPE on one head vector held as above (rope.wgsl:50-78, ropeRef
+// ops_ref.ts:65-92), with cs[j] = rope_cos_sin(inv_freq[j], pos) for the
+// vector's position precomputed in LDS (one table per position, shared by
+// all heads of a token). NEOX pairs (j, j + D/2): for D = 128 both halves sit
+// in the same lane; for D = 64 the partner is lane l ^ 32. NORM pairs (2j,
+// 2j+1): the partner is lane l ^ 1.
 template <int D>
-__device__ __forceinline__ void head_rope(float& e0, float& e1, const float* __restrict__ inv_freq,
-                                          int pos, int pairing, int lane) {
+__device__ __forceinline__ void head_rope(float& e0, float& e1, const float2* cs, int pairing,
+                                          int lane) {
   constexpr int half = D / 2;
   if (pairing == FLK_ROPE_NORM) {
     const float p0 = shfl_xor(e0, 1);
     const float p1 = (D == 128) ? shfl_xor(e1, 1) : 0.f;
     const bool first = (lane & 1) == 0;
-    if (lane < D) e0 = rope_elem(e0, p0, first, inv_freq[lane >> 1], pos);
-    if (D == 128) e1 = rope_elem(e1, p1, first, inv_freq[(lane + 64) >> 1], pos);
+    if (lane < D) e0 = rope_rot(e0, p0, first, cs[lane >> 1]);
+    if (D == 128) e1 = rope_rot(e1, p1, first, cs[(lane + 64) >> 1]);
   } else if (D == 128) {
     const float a = e0, b = e1;  // elements j = lane and j + 64
-    e0 = rope_elem(a, b, true, inv_freq[lane], pos);
-    e1 = rope_elem(b, a, false, inv_freq[lane], pos);
+    const float2 c = cs[lane];
+    e0 = rope_rot(a, b, true, c);
+    e1 = rope_rot(b, a, false, c);
   } else {
     const float p0 = shfl_xor(e0, 32);
     const bool first = lane < half;
-    e0 = rope_elem(e0, p0, first, inv_freq[first ? lane : lane - half], pos);
+    e0 = rope_rot(e0, p0, first, cs[first ? lane : lane - half]);
   }
 }
 

@@ -4,27 +4,34 @@
 // per q-head and holds every score in workgroup memory, which caps context at
 // $MAX_KEYS and leaves the GPU with 16 workgroups. Here two launches:
 //
-// decode_split_kernel  grid (n_kv_heads, n_splits, n_seqs), 256 threads.
-//   One workgroup streams keys [t0, t1) of one kv head and serves all G =
-//   n_heads / n_kv_heads query heads that read it, so each K/V byte is read
-//   from HBM once. Each K/V row of one kv head (D floats) is loaded by D/4
-//   lanes as float4 -- one coalesced 512 B segment for D = 128 -- so a
-//   workgroup has 256 / (D/4) "slots", slot s taking keys t0 + s, t0 + s +
-//   SLOTS, ..., and U keys per slot are in flight per iteration.
-//   Scores: per-lane float4 dot, then a DPP/swizzle sum over the row's lanes;
-//   online softmax (running max m, denominator l, unnormalised accumulator)
-//   per slot; the slots merge through LDS. A single-split row writes o
-//   directly, otherwise the workgroup writes its (m, l, acc) partial.
-// decode_merge_kernel  grid (n_heads, n_seqs), 256 threads: combines the
-//   partials of one head with log-sum-exp weights (rows of a single split exit).
+// decode_split_kernel<D, G, KH>  grid (n_kv_heads / KH, n_splits, n_seqs),
+//   256 threads. A workgroup streams a share of the keys of KH adjacent kv heads and
+//   serves the KH * G query heads that read them (G = n_heads / n_kv_heads),
+//   so each K/V byte is read from HBM once. The cache row of one (key, kv head)
+//   is D floats, loaded by D/4 lanes as float4: a "slot". The 256 / (D/4)
+//   slots are KH kv heads x PH key phases; with KH = n_kv_heads (8 for
+//   Qwen3-0.6B) and D = 128 a workgroup reads whole 4 KB cache rows, one key
+//   after another, as one contiguous stream per K and V.
+//   Keys go to workgroups in blocks of PH * U, dealt round-robin over the
+//   splits, so the launch sweeps the cache front to back as one window.
+//   Per iteration a slot holds U keys in registers, and the next iteration's
+//   keys are loaded before the current ones are used (two register sets). The
+//   first set is requested before the prologue runs, so HBM latency overlaps
+//   it. Scores: per-lane float4 dot, then a DPP/swizzle sum over the slot's
+//   lanes; online softmax (running max m, denominator l, unnormalised
+//   accumulator) per slot; phases of one kv head merge through LDS. A
+//   single-split sequence writes o directly, otherwise each head writes its
+//   (m, l, acc) partial.
+// decode_merge_kernel  grid (n_heads, D / 32, n_seqs): combines the partials of
+//   one head with log-sum-exp weights in one round of loads.
 // The two launches are ordered by the stream: no atomics or device-scope fences
 // inside a launch.
 //
 // Fused mode (flk_decode_layer) prepends Layer.encode's prologue
-// (layer.ts:598-622): every workgroup recomputes q's per-head RMSNorm + RoPE
-// for its G heads (a few hundred flops), and the workgroup whose key range
-// holds position pos also normalises/rotates the new k row and writes k and v
-// into the cache before streaming keys.
+// (layer.ts:598-622): every workgroup computes q's per-head RMSNorm + RoPE for
+// its KH * G heads, and the workgroup whose key range holds position pos also
+// normalises/rotates the new k rows and writes k and v into the cache row pos;
+// it uses those rows from LDS rather than reading them back.
 #include <float.h>
 
 #include "common.hpp"
@@ -60,15 +67,24 @@ struct DecodeArgs {
 };
 
 // Launch-shape tunables (compile-time; the defaults are the measured choice).
+#ifndef FLK_DECODE_TARGET_WG
+#define FLK_DECODE_TARGET_WG 256
+#endif
+#ifndef FLK_DECODE_RAGGED_TARGET_WG
+#define FLK_DECODE_RAGGED_TARGET_WG 1024
+#endif
 #ifndef FLK_DECODE_UNROLL
 #define FLK_DECODE_UNROLL 8
 #endif
-#ifndef FLK_DECODE_TARGET_WG
-#define FLK_DECODE_TARGET_WG 1024
-#endif
 constexpr int kDecodeThreads = 256;
-constexpr int kDecodeUnroll = FLK_DECODE_UNROLL;
 constexpr int kMergeThreads = 256;
+constexpr int kMergeCols = 8;    // float4 columns per merge workgroup (32 channels)
+constexpr int kMergeBatch = 8;   // splits per thread per round of loads
+
+// Keys per slot per iteration: fewer when G is large, to bound registers.
+__host__ __device__ constexpr int decode_unroll(int G) {
+  return G <= 2 ? FLK_DECODE_UNROLL : (G <= 4 ? 4 : 2);
+}
 
 // Keys sequence `seq` attends: the argument for one sequence; for a ragged
 // batch its n_keys entry, clamped to the planned bound so that the grid covers
@@ -77,90 +93,219 @@ __device__ __forceinline__ uint32_t seq_keys(const DecodeArgs& a, uint32_t seq) 
   return a.n_keys_dev != nullptr ? min(a.n_keys_dev[seq], a.n_keys) : a.n_keys;
 }
 
-template <int D, int G>
-__global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs a) {
-  constexpr int LPK = D / 4;                    // lanes per key row
-  constexpr int SLOTS = kDecodeThreads / LPK;   // concurrent keys per workgroup
-  constexpr int U = kDecodeUnroll;
-  constexpr int NT = G * LPK;                   // (head, float4 column) items
+// U keys of one slot: rows base + u * PH + ph. Past the end of the split the
+// last row (t1 - 1) is loaded again instead, so every load is unconditional;
+// attend_keys masks those keys out.
+template <int U, int PH>
+__device__ __forceinline__ void load_keys(float4 (&kr)[U], float4 (&vr)[U], const float4* kb,
+                                          const float4* vb, size_t row4, uint32_t base, int ph,
+                                          uint32_t t1) {
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint32_t t = min(base + u * PH + ph, t1 - 1);
+    kr[u] = kb[(size_t)t * row4];
+    vr[u] = vb[(size_t)t * row4];
+  }
+}
 
-  __shared__ float4 s_q[G][LPK];
-  __shared__ float s_m[SLOTS][G];
-  __shared__ float s_l[SLOTS][G];
-  __shared__ float4 s_acc[SLOTS][G][LPK];
+// Online-softmax update of one slot's G heads with U keys. The row at `pos`
+// (when this workgroup appended it) is taken from knew / vnew.
+template <int D, int G, int U, int PH>
+__device__ __forceinline__ void attend_keys(const float4 (&kr_in)[U], const float4 (&vr_in)[U],
+                                            const float4 (&qv)[G], float (&m)[G], float (&l)[G],
+                                            float4 (&acc)[G], uint32_t base, int ph, uint32_t t1,
+                                            bool owns_pos, uint32_t pos, float4 knew, float4 vnew,
+                                            float scale) {
+  constexpr int LPK = D / 4;
+  float4 kr[U], vr[U];
+  float s[G][U];
+#pragma unroll
+  for (int u = 0; u < U; u++) {
+    const uint32_t t = base + u * PH + ph;
+    const bool mine = owns_pos && t == pos;
+    kr[u] = mine ? knew : kr_in[u];
+    vr[u] = mine ? vnew : vr_in[u];
+    const bool valid = t < t1;
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      float d = qv[g].x * kr[u].x;
+      d = fmaf(qv[g].y, kr[u].y, d);
+      d = fmaf(qv[g].z, kr[u].z, d);
+      d = fmaf(qv[g].w, kr[u].w, d);
+      d = group_sum<LPK>(d);
+      s[g][u] = valid ? d * scale : -INFINITY;
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; g++) {
+    float cm = s[g][0];
+#pragma unroll
+    for (int u = 1; u < U; u++) cm = fmaxf(cm, s[g][u]);
+    const float mn = fmaxf(m[g], cm);
+    if (mn == -INFINITY) continue;  // no valid key yet in this slot
+    const float corr = expf(m[g] - mn);
+    l[g] *= corr;
+    acc[g].x *= corr;
+    acc[g].y *= corr;
+    acc[g].z *= corr;
+    acc[g].w *= corr;
+#pragma unroll
+    for (int u = 0; u < U; u++) {
+      const float e = expf(s[g][u] - mn);
+      l[g] += e;
+      acc[g].x = fmaf(e, vr[u].x, acc[g].x);
+      acc[g].y = fmaf(e, vr[u].y, acc[g].y);
+      acc[g].z = fmaf(e, vr[u].z, acc[g].z);
+      acc[g].w = fmaf(e, vr[u].w, acc[g].w);
+    }
+    m[g] = mn;
+  }
+}
+
+template <int D, int G, int KH>
+__global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs a) {
+  constexpr int LPK = D / 4;                    // lanes per (key, kv head) row
+  constexpr int SLOTS = kDecodeThreads / LPK;   // 8 (D = 128) or 16 (D = 64)
+  static_assert(SLOTS % KH == 0, "KH must divide the slot count");
+  constexpr int PH = SLOTS / KH;                // key phases
+  constexpr int U = decode_unroll(G);
+  constexpr int KPI = PH * U;                   // keys per iteration
+  constexpr int HG = KH * G;                    // q heads of this workgroup
+
+  __shared__ float4 s_q[HG][LPK];
+  __shared__ float4 s_knew[KH][LPK];
+  __shared__ float4 s_vnew[KH][LPK];
+  __shared__ float2 s_cs[D / 2];  // fused: RoPE cos/sin at the new position
+  __shared__ float s_m[PH > 1 ? SLOTS : 1][G];
+  __shared__ float s_l[PH > 1 ? SLOTS : 1][G];
+  __shared__ float4 s_acc[PH > 1 ? SLOTS : 1][G][LPK];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int slot = tid / LPK;
   const int sl = tid % LPK;
-  const uint32_t kvh = blockIdx.x;
+  const int kh = slot % KH;
+  const int ph = slot / KH;
+  const uint32_t kvh0 = blockIdx.x * KH;
+  const uint32_t kvh = kvh0 + kh;
   const uint32_t split = blockIdx.y;
   const uint32_t seq = blockIdx.z;
-  const uint32_t h0 = kvh * G;  // first q head of this group
+  const uint32_t h0 = kvh0 * G;  // first q head of this workgroup
 
   const uint32_t n_keys = seq_keys(a, seq);
   const uint64_t row0 = a.seq_row_off != nullptr ? a.seq_row_off[seq] : 0;
   if (n_keys == 0) {  // empty ragged sequence: zero output rows
     if (split == 0)
-      for (int i = tid; i < G * D; i += kDecodeThreads)
+      for (int i = tid; i < HG * D; i += kDecodeThreads)
         a.o[((size_t)seq * a.n_heads + h0) * D + i] = 0.f;
     return;
   }
   const uint32_t n_splits = (n_keys + a.kps - 1) / a.kps;
   if (split >= n_splits) return;  // uniform per workgroup
-  const uint32_t t0 = split * a.kps;
-  const uint32_t t1 = min(t0 + a.kps, n_keys);
-  const size_t row = (size_t)a.n_kv_heads * D;  // floats per cache row
+  // Blocks of KPI keys are dealt round-robin: split s takes blocks s, s +
+  // n_splits, ..., so at any time the workgroups of a launch read neighbouring
+  // blocks (one moving window of the cache rather than n_splits streams).
+  const uint32_t n_blocks = (n_keys + KPI - 1) / KPI;
+  const uint32_t t1 = n_keys;
+  const size_t row4 = (size_t)a.n_kv_heads * (D / 4);  // float4 per cache row
 
-  // ---- q for the G heads (fused: prologue computed here) -------------------
-  if (a.q_raw != nullptr) {
-    const uint32_t pos = n_keys - 1;
-    const bool owns_pos = pos >= t0 && pos < t1;
-    const int n_vec = G + (owns_pos ? 2 : 0);
-    for (int vi = wave; vi < n_vec; vi += kDecodeThreads / 64) {
-      float e0, e1;
-      if (vi < G) {  // q head h0 + vi
-        const float* src = a.q_raw + (size_t)(h0 + vi) * D;
-        e0 = lane < D ? src[lane] : 0.f;
-        e1 = D == 128 ? src[lane + 64] : 0.f;
-        head_rmsnorm<D>(e0, e1, a.gq, lane, a.eps);
-        head_rope<D>(e0, e1, a.inv_freq, (int)pos, a.pairing, lane);
-        float* sq = reinterpret_cast<float*>(&s_q[vi][0]);
-        if (lane < D) sq[lane] = e0;
-        if (D == 128) sq[lane + 64] = e1;
-        if (split == 0) {
-          float* dq = a.qn_out + (size_t)(h0 + vi) * D;
-          if (lane < D) dq[lane] = e0;
-          if (D == 128) dq[lane + 64] = e1;
-        }
-      } else if (vi == G) {  // new k row of this kv head -> kcache[pos]
-        const float* src = a.k_raw + (size_t)kvh * D;
-        e0 = lane < D ? src[lane] : 0.f;
-        e1 = D == 128 ? src[lane + 64] : 0.f;
-        head_rmsnorm<D>(e0, e1, a.gk, lane, a.eps);
-        head_rope<D>(e0, e1, a.inv_freq, (int)pos, a.pairing, lane);
-        float* dk = a.kcache_w + (size_t)pos * row + (size_t)kvh * D;
-        if (lane < D) dk[lane] = e0;
-        if (D == 128) dk[lane + 64] = e1;
-      } else {  // new v row, raw
-        const float* src = a.v_raw + (size_t)kvh * D;
-        float* dv = a.vcache_w + (size_t)pos * row + (size_t)kvh * D;
-        if (lane < D) dv[lane] = src[lane];
-        if (D == 128) dv[lane + 64] = src[lane + 64];
+  // vmcnt retires loads in issue order, so everything the prologue reads is
+  // requested BEFORE the first K/V rows: the prologue then waits only for its
+  // own inputs while the rows stream in. Inputs are staged through LDS.
+  constexpr int QLD = (HG * LPK + kDecodeThreads - 1) / kDecodeThreads;  // q float4 / thread
+  constexpr int KLD = (KH * LPK + kDecodeThreads - 1) / kDecodeThreads;  // new-row float4
+  const bool fused = a.q_raw != nullptr;
+  const uint32_t pos = n_keys - 1;  // the appended row (fused)
+  const bool owns_pos = fused && (pos / KPI) % n_splits == split;
+  float4 qld[QLD], kld[KLD], vld[KLD];
+  float gq0 = 0.f, gq1 = 0.f, gk0 = 0.f, gk1 = 0.f, invf = 0.f;
+  {
+    const float4* qs = reinterpret_cast<const float4*>(
+        fused ? a.q_raw + (size_t)h0 * D : a.q + ((size_t)seq * a.n_heads + h0) * D);
+#pragma unroll
+    for (int i = 0; i < QLD; i++) qld[i] = qs[min(tid + kDecodeThreads * i, HG * LPK - 1)];
+  }
+  if (fused) {
+    const float4* ks = reinterpret_cast<const float4*>(a.k_raw + (size_t)kvh0 * D);
+    const float4* vs = reinterpret_cast<const float4*>(a.v_raw + (size_t)kvh0 * D);
+#pragma unroll
+    for (int i = 0; i < KLD; i++) {
+      const int f = min(tid + kDecodeThreads * i, KH * LPK - 1);
+      kld[i] = ks[f];
+      vld[i] = vs[f];
+    }
+    gq0 = a.gq[lane];
+    gk0 = a.gk[lane];
+    if (D == 128) {
+      gq1 = a.gq[lane + 64];
+      gk1 = a.gk[lane + 64];
+    }
+    invf = a.inv_freq[min(tid, D / 2 - 1)];
+  }
+
+  const float4* kb = reinterpret_cast<const float4*>(a.kcache) + row0 * row4 + (size_t)kvh * LPK + sl;
+  const float4* vb = reinterpret_cast<const float4*>(a.vcache) + row0 * row4 + (size_t)kvh * LPK + sl;
+  float4 ka[U], va[U], kn[U], vn[U];
+  load_keys<U, PH>(ka, va, kb, vb, row4, split * KPI, ph, t1);
+
+  // ---- q for the KH * G heads (fused: prologue computed here) --------------
+  // Unconditional stores (clamped index: surplus threads rewrite the last
+  // element with the value they loaded from it), so the loads above have no
+  // conditional use to be sunk into, past the row loads.
+#pragma unroll
+  for (int i = 0; i < QLD; i++) {
+    const int f = min(tid + kDecodeThreads * i, HG * LPK - 1);
+    s_q[f / LPK][f % LPK] = qld[i];
+  }
+  if (fused) {
+#pragma unroll
+    for (int i = 0; i < KLD; i++) {
+      const int f = min(tid + kDecodeThreads * i, KH * LPK - 1);
+      s_knew[f / LPK][f % LPK] = kld[i];
+      s_vnew[f / LPK][f % LPK] = vld[i];
+    }
+    if (tid < D / 2) s_cs[tid] = rope_cos_sin(invf, pos);
+    __syncthreads();
+    for (int vi = wave; vi < HG; vi += kDecodeThreads / 64) {  // q head h0 + vi
+      float* sq = reinterpret_cast<float*>(&s_q[vi][0]);
+      float e0 = sq[lane], e1 = D == 128 ? sq[lane + 64] : 0.f;
+      head_rmsnorm<D>(e0, e1, gq0, gq1, a.eps);
+      head_rope<D>(e0, e1, s_cs, a.pairing, lane);
+      sq[lane] = e0;
+      if (D == 128) sq[lane + 64] = e1;
+      if (split == 0) {
+        float* dq = a.qn_out + (size_t)(h0 + vi) * D;
+        dq[lane] = e0;
+        if (D == 128) dq[lane + 64] = e1;
       }
     }
-  } else {
-    for (int i = tid; i < NT; i += kDecodeThreads) {
-      const int g = i / LPK, c = i % LPK;
-      s_q[g][c] = reinterpret_cast<const float4*>(a.q + ((size_t)seq * a.n_heads + h0 + g) * D)[c];
+    if (owns_pos) {  // append row pos: k normed + rotated, v raw (layer.ts:616-622)
+      const size_t row = (size_t)a.n_kv_heads * D;
+      for (int j = wave; j < KH; j += kDecodeThreads / 64) {
+        float* lk = reinterpret_cast<float*>(&s_knew[j][0]);
+        const float* lv = reinterpret_cast<const float*>(&s_vnew[j][0]);
+        float e0 = lk[lane], e1 = D == 128 ? lk[lane + 64] : 0.f;
+        head_rmsnorm<D>(e0, e1, gk0, gk1, a.eps);
+        head_rope<D>(e0, e1, s_cs, a.pairing, lane);
+        float* dk = a.kcache_w + (size_t)pos * row + (size_t)(kvh0 + j) * D;
+        float* dv = a.vcache_w + (size_t)pos * row + (size_t)(kvh0 + j) * D;
+        dk[lane] = lk[lane] = e0;
+        dv[lane] = lv[lane];
+        if (D == 128) {
+          dk[lane + 64] = lk[lane + 64] = e1;
+          dv[lane + 64] = lv[lane + 64];
+        }
+      }
     }
   }
-  __syncthreads();  // s_q ready; fused cache writes visible to this workgroup
+  __syncthreads();  // s_q (and the new k/v rows) ready
 
   float4 qv[G];
 #pragma unroll
-  for (int g = 0; g < G; g++) qv[g] = s_q[g][sl];
+  for (int g = 0; g < G; g++) qv[g] = s_q[kh * G + g][sl];
+  const float4 knew = s_knew[kh][sl];
+  const float4 vnew = s_vnew[kh][sl];
 
   float m[G], l[G];
   float4 acc[G];
@@ -171,64 +316,39 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs
     acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
   }
 
-  const float4* kb = reinterpret_cast<const float4*>(a.kcache + row0 * row + (size_t)kvh * D) + sl;
-  const float4* vb = reinterpret_cast<const float4*>(a.vcache + row0 * row + (size_t)kvh * D) + sl;
-  const size_t row4 = row / 4;
-
-  for (uint32_t base = t0; base < t1; base += SLOTS * U) {
-    float4 kr[U], vr[U];
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const uint32_t t = base + u * SLOTS + slot;
-      if (t < t1) {
-        kr[u] = kb[(size_t)t * row4];
-        vr[u] = vb[(size_t)t * row4];
-      } else {
-        kr[u] = make_float4(0.f, 0.f, 0.f, 0.f);
-        vr[u] = kr[u];
-      }
-    }
-    float s[G][U];
-#pragma unroll
-    for (int u = 0; u < U; u++) {
-      const bool valid = base + u * SLOTS + slot < t1;
-#pragma unroll
-      for (int g = 0; g < G; g++) {
-        float d = qv[g].x * kr[u].x;
-        d = fmaf(qv[g].y, kr[u].y, d);
-        d = fmaf(qv[g].z, kr[u].z, d);
-        d = fmaf(qv[g].w, kr[u].w, d);
-        d = group_sum<LPK>(d);
-        s[g][u] = valid ? d * a.scale : -INFINITY;
-      }
-    }
-#pragma unroll
-    for (int g = 0; g < G; g++) {
-      float cm = s[g][0];
-#pragma unroll
-      for (int u = 1; u < U; u++) cm = fmaxf(cm, s[g][u]);
-      const float mn = fmaxf(m[g], cm);
-      if (mn == -INFINITY) continue;  // no valid key yet in this slot
-      const float corr = expf(m[g] - mn);
-      l[g] *= corr;
-      acc[g].x *= corr;
-      acc[g].y *= corr;
-      acc[g].z *= corr;
-      acc[g].w *= corr;
-#pragma unroll
-      for (int u = 0; u < U; u++) {
-        const float e = expf(s[g][u] - mn);
-        l[g] += e;
-        acc[g].x = fmaf(e, vr[u].x, acc[g].x);
-        acc[g].y = fmaf(e, vr[u].y, acc[g].y);
-        acc[g].z = fmaf(e, vr[u].z, acc[g].z);
-        acc[g].w = fmaf(e, vr[u].w, acc[g].w);
-      }
-      m[g] = mn;
-    }
+  // Two register sets: the next block's loads are issued before the current
+  // block's arithmetic. Loads are unconditional (a block past the end re-reads
+  // the current one, which is in cache) so the compiler can count them.
+  for (uint32_t b = split; b < n_blocks; b += 2 * n_splits) {
+    const uint32_t b1 = b + n_splits;
+    const uint32_t b2 = b1 + n_splits;
+    load_keys<U, PH>(kn, vn, kb, vb, row4, (b1 < n_blocks ? b1 : b) * KPI, ph, t1);
+    attend_keys<D, G, U, PH>(ka, va, qv, m, l, acc, b * KPI, ph, t1, owns_pos, pos, knew, vnew,
+                             a.scale);
+    load_keys<U, PH>(ka, va, kb, vb, row4, (b2 < n_blocks ? b2 : b) * KPI, ph, t1);
+    if (b1 < n_blocks)
+      attend_keys<D, G, U, PH>(kn, vn, qv, m, l, acc, b1 * KPI, ph, t1, owns_pos, pos, knew,
+                               vnew, a.scale);
   }
 
-  // ---- merge the slots of this workgroup --------------------------------
+  // ---- combine the phases of each kv head, write o or the partial ---------
+  // hq: q head within the workgroup (kv head j = hq / G, group member hq % G).
+  auto emit = [&](int hq, int c, float M, float L, float4 A) {
+    const uint32_t h = h0 + (uint32_t)hq;
+    if (n_splits == 1) {
+      reinterpret_cast<float4*>(a.o + ((size_t)seq * a.n_heads + h) * D)[c] =
+          make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
+    } else {
+      const size_t p = ((size_t)seq * a.n_heads + h) * a.max_splits + split;
+      if (c == 0) a.part_ml[p] = make_float2(M, L);
+      reinterpret_cast<float4*>(a.part_acc + p * D)[c] = A;
+    }
+  };
+  if (PH == 1) {
+#pragma unroll
+    for (int g = 0; g < G; g++) emit(kh * G + g, sl, m[g], l[g], acc[g]);
+    return;
+  }
   if (sl == 0) {
 #pragma unroll
     for (int g = 0; g < G; g++) {
@@ -239,107 +359,145 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs
 #pragma unroll
   for (int g = 0; g < G; g++) s_acc[slot][g][sl] = acc[g];
   __syncthreads();
-
-  for (int i = tid; i < NT; i += kDecodeThreads) {
-    const int g = i / LPK, c = i % LPK;
+  for (int i = tid; i < HG * LPK; i += kDecodeThreads) {
+    const int hq = i / LPK, c = i % LPK;  // hq = kv-head-in-group * G + g
+    const int j = hq / G, g = hq % G;
     float M = -INFINITY;
-    for (int s = 0; s < SLOTS; s++) M = fmaxf(M, s_m[s][g]);
+#pragma unroll
+    for (int p = 0; p < PH; p++) M = fmaxf(M, s_m[j + KH * p][g]);
     float L = 0.f;
     float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-    for (int s = 0; s < SLOTS; s++) {
-      const float ms = s_m[s][g];
+#pragma unroll
+    for (int p = 0; p < PH; p++) {
+      const int sidx = j + KH * p;
+      const float ms = s_m[sidx][g];
       const float w = ms == -INFINITY ? 0.f : expf(ms - M);
-      L = fmaf(s_l[s][g], w, L);
-      const float4 as = s_acc[s][g][c];
+      L = fmaf(s_l[sidx][g], w, L);
+      const float4 as = s_acc[sidx][g][c];
       A.x = fmaf(as.x, w, A.x);
       A.y = fmaf(as.y, w, A.y);
       A.z = fmaf(as.z, w, A.z);
       A.w = fmaf(as.w, w, A.w);
     }
-    if (n_splits == 1) {
-      const float4 r = make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
-      reinterpret_cast<float4*>(a.o + ((size_t)seq * a.n_heads + h0 + g) * D)[c] = r;
-    } else {
-      const size_t p = ((size_t)seq * a.n_heads + h0 + g) * a.max_splits + split;
-      if (c == 0) a.part_ml[p] = make_float2(M, L);
-      reinterpret_cast<float4*>(a.part_acc + p * D)[c] = A;
-    }
+    emit(hq, c, M, L, A);
   }
 }
 
-// One workgroup per (head, sequence). Thread -> (group, float4 column): group
-// r folds splits r, r + GROUPS, ... with weights exp(m_s - M) against the
-// global max M; the groups then add up through LDS in a fixed order, so the
-// result does not depend on scheduling.
+// grid (head, column chunk, sequence); thread -> (group r, float4 column c).
+// Group r takes splits r, r + GROUPS, ...: each round issues up to
+// kMergeBatch independent loads per thread, folds them with weights against
+// the running max, and the groups combine through LDS in a fixed order (the
+// result does not depend on scheduling).
 template <int D>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs a) {
-  constexpr int LPK = D / 4;
-  constexpr int GROUPS = kMergeThreads / LPK;
-  __shared__ float s_max[GROUPS];
+  constexpr int GROUPS = kMergeThreads / kMergeCols;
+  __shared__ float s_m[GROUPS];
   __shared__ float s_l[GROUPS];
-  __shared__ float4 s_acc[GROUPS][LPK];
+  __shared__ float4 s_acc[GROUPS][kMergeCols];
 
   const uint32_t head = blockIdx.x;
-  const uint32_t seq = blockIdx.y;
+  const uint32_t seq = blockIdx.z;
   const uint32_t n_keys = seq_keys(a, seq);
   const uint32_t n_splits = (n_keys + a.kps - 1) / a.kps;
   if (n_splits <= 1) return;  // written by the split kernel (or empty)
   const int tid = threadIdx.x;
-  const int grp = tid / LPK, c = tid % LPK;
+  const int grp = tid / kMergeCols;
+  const int c = blockIdx.y * kMergeCols + tid % kMergeCols;  // float4 column
   const size_t p0 = ((size_t)seq * a.n_heads + head) * a.max_splits;
 
-  float M = -INFINITY;
-  for (uint32_t s = grp; s < n_splits; s += GROUPS) M = fmaxf(M, a.part_ml[p0 + s].x);
-  if (c == 0) s_max[grp] = M;
-  __syncthreads();
-  M = s_max[0];
-#pragma unroll
-  for (int r = 1; r < GROUPS; r++) M = fmaxf(M, s_max[r]);
-
-  float L = 0.f;
+  float M = -INFINITY, L = 0.f;
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (uint32_t s = grp; s < n_splits; s += GROUPS) {
-    const float2 ml = a.part_ml[p0 + s];
-    const float w = ml.x == -INFINITY ? 0.f : expf(ml.x - M);
-    const float4 p = reinterpret_cast<const float4*>(a.part_acc + (p0 + s) * D)[c];
-    L = fmaf(ml.y, w, L);
+  for (uint32_t s0 = grp; s0 < n_splits; s0 += GROUPS * kMergeBatch) {
+    float2 ml[kMergeBatch];
+    float4 pa[kMergeBatch];
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; i++) {
+      const uint32_t s = s0 + GROUPS * i;
+      if (s < n_splits) {
+        ml[i] = a.part_ml[p0 + s];
+        pa[i] = reinterpret_cast<const float4*>(a.part_acc + (p0 + s) * D)[c];
+      } else {
+        ml[i] = make_float2(-INFINITY, 0.f);
+        pa[i] = make_float4(0.f, 0.f, 0.f, 0.f);
+      }
+    }
+    float mx = M;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; i++) mx = fmaxf(mx, ml[i].x);
+    if (mx == -INFINITY) continue;
+    const float wo = M == -INFINITY ? 0.f : expf(M - mx);
+    L *= wo;
+    A.x *= wo;
+    A.y *= wo;
+    A.z *= wo;
+    A.w *= wo;
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; i++) {
+      const float w = ml[i].x == -INFINITY ? 0.f : expf(ml[i].x - mx);
+      L = fmaf(ml[i].y, w, L);
+      A.x = fmaf(pa[i].x, w, A.x);
+      A.y = fmaf(pa[i].y, w, A.y);
+      A.z = fmaf(pa[i].z, w, A.z);
+      A.w = fmaf(pa[i].w, w, A.w);
+    }
+    M = mx;
+  }
+  if (tid % kMergeCols == 0) {
+    s_m[grp] = M;
+    s_l[grp] = L;
+  }
+  s_acc[grp][tid % kMergeCols] = A;
+  __syncthreads();
+  if (grp != 0) return;
+  float MM = -INFINITY;
+#pragma unroll
+  for (int r = 0; r < GROUPS; r++) MM = fmaxf(MM, s_m[r]);
+  L = 0.f;
+  A = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+  for (int r = 0; r < GROUPS; r++) {
+    const float mr = s_m[r];
+    const float w = mr == -INFINITY ? 0.f : expf(mr - MM);
+    L = fmaf(s_l[r], w, L);
+    const float4 p = s_acc[r][tid];
     A.x = fmaf(p.x, w, A.x);
     A.y = fmaf(p.y, w, A.y);
     A.z = fmaf(p.z, w, A.z);
     A.w = fmaf(p.w, w, A.w);
-  }
-  if (c == 0) s_l[grp] = L;
-  s_acc[grp][c] = A;
-  __syncthreads();
-  if (grp != 0) return;
-  L = s_l[0];
-  A = s_acc[0][c];
-#pragma unroll
-  for (int r = 1; r < GROUPS; r++) {
-    L += s_l[r];
-    const float4 p = s_acc[r][c];
-    A.x += p.x;
-    A.y += p.y;
-    A.z += p.z;
-    A.w += p.w;
   }
   reinterpret_cast<float4*>(a.o + ((size_t)seq * a.n_heads + head) * D)[c] =
       make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
 }
 
 // ------------------------------------------------------------------ plan ----
-// Keys per split: aim for ~kTargetWG split workgroups in total (several per CU
-// so that enough 512 B rows are in flight to cover HBM latency), in multiples
-// of one loop iteration (SLOTS * U keys), and at least kMinKps keys.
+// KH: kv heads per workgroup, the largest of 8, 4, 2, 1 dividing n_kv_heads.
+static uint32_t kv_heads_per_wg(uint32_t n_kv_heads) {
+  for (uint32_t kh = 8; kh > 1; kh >>= 1)
+    if (n_kv_heads % kh == 0) return kh;
+  return 1;
+}
+
+// Keys per loop iteration of one workgroup (PH * U).
+static uint32_t keys_per_iter(const DecodeShape& s) {
+  const uint32_t slots = kDecodeThreads / (s.head_dim / 4);
+  const uint32_t U = decode_unroll((int)(s.n_heads / s.n_kv_heads));
+  return slots / kv_heads_per_wg(s.n_kv_heads) * U;
+}
+
+// Keys per split: aim for a fixed number of split workgroups in total (one or
+// two per CU stream best; more only queue up), in whole loop iterations and at
+// least four of them. A ragged batch plans from its longest sequence, so it
+// asks for more, shorter splits to keep short sequences from idling CUs.
 constexpr uint32_t kTargetWG = FLK_DECODE_TARGET_WG;
-constexpr uint32_t kMinKps = 128;
+constexpr uint32_t kRaggedTargetWG = FLK_DECODE_RAGGED_TARGET_WG;
 
 uint32_t decode_keys_per_split(const DecodeShape& s) {
-  const uint64_t work = (uint64_t)s.max_n_keys * s.n_kv_heads * s.n_seqs;
-  uint64_t kps = (work + kTargetWG - 1) / kTargetWG;
-  const uint64_t q = 64;  // SLOTS * U for D = 128 (and a divisor of it for 64)
-  kps = (kps + q - 1) / q * q;
-  if (kps < kMinKps) kps = kMinKps;
+  const uint64_t kpi = keys_per_iter(s);
+  const uint64_t units = (uint64_t)(s.n_kv_heads / kv_heads_per_wg(s.n_kv_heads)) * s.n_seqs;
+  const uint64_t target = s.n_seqs > 1 ? kRaggedTargetWG : kTargetWG;
+  uint64_t kps = ((uint64_t)s.max_n_keys * units + target - 1) / target;
+  kps = (kps + kpi - 1) / kpi * kpi;
+  if (kps < 4 * kpi) kps = 4 * kpi;
   return (uint32_t)kps;
 }
 
@@ -359,28 +517,31 @@ uint64_t decode_ws_bytes(const DecodeShape& s) {
   return ws_for_slots((uint64_t)s.n_seqs * s.n_heads * splits, s.head_dim);
 }
 
-// Bound over every call with n_keys <= s.max_n_keys and n_seqs <= s.n_seqs:
-// kps >= kMinKps and kps >= n_keys * n_kv_heads * n / kTargetWG for a call
-// with n sequences, so it has at most min(ceil(max / kMinKps), ceil(kTargetWG
-// / (n_kv_heads * n))) splits per sequence; take the largest n * splits.
+// Bound over every call with n_keys <= s.max_n_keys and n_seqs <= s.n_seqs
+// (single-sequence calls included). For n sequences kps >= max(4 * kpi,
+// n_keys * units / target), so a sequence has at most min(ceil(max_n_keys /
+// (4 * kpi)), ceil(target / units)) splits; take the largest n * splits.
 uint64_t decode_ws_bound(const DecodeShape& s) {
-  const uint64_t by_len = (s.max_n_keys + kMinKps - 1) / kMinKps;
+  const uint64_t kpi = keys_per_iter(s);
+  const uint64_t by_len = (s.max_n_keys + 4 * kpi - 1) / (4 * kpi);
+  const uint64_t groups = s.n_kv_heads / kv_heads_per_wg(s.n_kv_heads);
   uint64_t best = 0;
   for (uint64_t n = 1; n <= s.n_seqs; n++) {
-    const uint64_t per = (uint64_t)s.n_kv_heads * n;
-    const uint64_t by_wg = (kTargetWG + per - 1) / per;
-    const uint64_t slots = n * (by_len < by_wg ? by_len : by_wg);
-    if (slots > best) best = slots;
+    const uint64_t units = groups * n;
+    const uint64_t target = n > 1 ? kRaggedTargetWG : kTargetWG;
+    const uint64_t by_wg = (target + units - 1) / units;
+    const uint64_t splits = by_len < by_wg ? by_len : by_wg;
+    if (splits > 1 && n * splits > best) best = n * splits;
   }
-  return ws_for_slots(best * s.n_heads, s.head_dim);
+  return best ? ws_for_slots(best * s.n_heads, s.head_dim) : 0;
 }
 
-template <int D>
-static hipError_t launch_split_d(const DecodeArgs& a, dim3 grid, uint32_t G, hipStream_t st) {
+template <int D, int KH>
+static hipError_t launch_split_kh(const DecodeArgs& a, dim3 grid, uint32_t G, hipStream_t st) {
   switch (G) {
-#define FLK_CASE(g)                                                                         \
-  case g:                                                                                   \
-    hipLaunchKernelGGL((decode_split_kernel<D, g>), grid, dim3(kDecodeThreads), 0, st, a); \
+#define FLK_CASE(g)                                                                             \
+  case g:                                                                                       \
+    hipLaunchKernelGGL((decode_split_kernel<D, g, KH>), grid, dim3(kDecodeThreads), 0, st, a); \
     break;
     FLK_CASE(1)
     FLK_CASE(2)
@@ -395,6 +556,17 @@ static hipError_t launch_split_d(const DecodeArgs& a, dim3 grid, uint32_t G, hip
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_split_d(const DecodeArgs& a, dim3 grid, uint32_t G, uint32_t KH,
+                                 hipStream_t st) {
+  switch (KH) {
+    case 8: return launch_split_kh<D, 8>(a, grid, G, st);
+    case 4: return launch_split_kh<D, 4>(a, grid, G, st);
+    case 2: return launch_split_kh<D, 2>(a, grid, G, st);
+    default: return launch_split_kh<D, 1>(a, grid, G, st);
+  }
 }
 
 hipError_t launch_decode(const float* q, const float* kcache, const float* vcache, float* o,
@@ -433,12 +605,13 @@ hipError_t launch_decode(const float* q, const float* kcache, const float* vcach
     a.kcache_w = fused->kcache_w;
     a.vcache_w = fused->vcache_w;
   }
-  const dim3 grid(s.n_kv_heads, a.max_splits, s.n_seqs);
+  const uint32_t KH = kv_heads_per_wg(s.n_kv_heads);
+  const dim3 grid(s.n_kv_heads / KH, a.max_splits, s.n_seqs);
   const uint32_t G = s.n_heads / s.n_kv_heads;
-  hipError_t e = s.head_dim == 128 ? launch_split_d<128>(a, grid, G, st)
-                                   : launch_split_d<64>(a, grid, G, st);
+  hipError_t e = s.head_dim == 128 ? launch_split_d<128>(a, grid, G, KH, st)
+                                   : launch_split_d<64>(a, grid, G, KH, st);
   if (e != hipSuccess || a.max_splits <= 1) return e;
-  const dim3 mgrid(s.n_heads, s.n_seqs);
+  const dim3 mgrid(s.n_heads, s.head_dim / 4 / kMergeCols, s.n_seqs);
   if (s.head_dim == 128)
     hipLaunchKernelGGL(decode_merge_kernel<128>, mgrid, dim3(kMergeThreads), 0, st, a);
   else

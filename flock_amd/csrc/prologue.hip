@@ -56,9 +56,10 @@ __global__ __launch_bounds__(256) void rope_kernel(float* __restrict__ x,
   const size_t ia = base + (pairing == FLK_ROPE_NORM ? 2 * j : j);
   const size_t ib = base + (pairing == FLK_ROPE_NORM ? 2 * j + 1 : j + half);
   const float a = x[ia], b = x[ib];
-  const int pos = (int)(pos0 + token);
-  x[ia] = rope_elem(a, b, true, inv_freq[j], pos);
-  x[ib] = rope_elem(b, a, false, inv_freq[j], pos);
+  const uint32_t pos = pos0 + token;
+  const float2 cs = rope_cos_sin(inv_freq[j], pos);
+  x[ia] = rope_rot(a, b, true, cs);
+  x[ib] = rope_rot(b, a, false, cs);
 }
 
 hipError_t launch_rope(float* x, const float* inv_freq, uint32_t n_tokens, uint32_t n_heads,
@@ -84,51 +85,59 @@ hipError_t launch_kv_append(const float* kn, const float* v, float* kcache, floa
 }
 
 // --------------------------------------------------------- fused prologue ----
-// One wave per head vector. Vector id -> (token, kind): the first n_heads are
-// q heads (norm + rope -> qn_out), the next n_kv_heads are k heads (norm + rope
+// One workgroup per token (every head of a token shares its position): the
+// first D/2 threads put cos/sin of the token's D/2 RoPE angles in LDS, then
+// each wave takes head vectors. Vector id -> kind: the first n_heads are q
+// heads (norm + rope -> qn_out), the next n_kv_heads are k heads (norm + rope
 // -> kcache row pos0 + token), the last n_kv_heads are v heads (copied raw to
 // vcache). Identical arithmetic to rmsnorm_kernel + rope_kernel for head_dim
 // vectors, so the caches match the unfused path bit for bit.
+constexpr int kPrologueThreads = 256;
+
 template <int D>
-__global__ __launch_bounds__(256) void qk_prologue_kernel(
+__global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
     const float* __restrict__ q_raw, const float* __restrict__ k_raw,
     const float* __restrict__ v_raw, const float* __restrict__ gq, const float* __restrict__ gk,
     const float* __restrict__ inv_freq, float eps, int32_t pairing, float* __restrict__ qn_out,
-    float* __restrict__ kcache, float* __restrict__ vcache, uint32_t n_tokens, uint32_t pos0,
-    uint32_t n_heads, uint32_t n_kv_heads) {
+    float* __restrict__ kcache, float* __restrict__ vcache, uint32_t pos0, uint32_t n_heads,
+    uint32_t n_kv_heads) {
+  __shared__ float2 s_cs[D / 2];
   const int lane = threadIdx.x & 63;
-  const uint32_t per_tok = n_heads + 2 * n_kv_heads;
-  const uint64_t vec = (uint64_t)blockIdx.x * 4 + (threadIdx.x >> 6);
-  if (vec >= (uint64_t)n_tokens * per_tok) return;  // uniform per wave
-  const uint32_t tok = (uint32_t)(vec / per_tok);
-  const uint32_t idx = (uint32_t)(vec % per_tok);
+  const int wave = threadIdx.x >> 6;
+  const uint32_t tok = blockIdx.x;
   const uint32_t pos = pos0 + tok;
+  if (threadIdx.x < D / 2) s_cs[threadIdx.x] = rope_cos_sin(inv_freq[threadIdx.x], pos);
+  __syncthreads();
+
+  const uint32_t per_tok = n_heads + 2 * n_kv_heads;
   const size_t kv_row = (size_t)n_kv_heads * D;
-  const float* src;
-  float* dst;
-  const float* g = nullptr;
-  if (idx < n_heads) {
-    src = q_raw + ((size_t)tok * n_heads + idx) * D;
-    dst = qn_out + ((size_t)tok * n_heads + idx) * D;
-    g = gq;
-  } else if (idx < n_heads + n_kv_heads) {
-    const uint32_t h = idx - n_heads;
-    src = k_raw + (size_t)tok * kv_row + (size_t)h * D;
-    dst = kcache + (size_t)pos * kv_row + (size_t)h * D;
-    g = gk;
-  } else {
-    const uint32_t h = idx - n_heads - n_kv_heads;
-    src = v_raw + (size_t)tok * kv_row + (size_t)h * D;
-    dst = vcache + (size_t)pos * kv_row + (size_t)h * D;
+  for (uint32_t idx = wave; idx < per_tok; idx += kPrologueThreads / 64) {
+    const float* src;
+    float* dst;
+    const float* g = nullptr;
+    if (idx < n_heads) {
+      src = q_raw + ((size_t)tok * n_heads + idx) * D;
+      dst = qn_out + ((size_t)tok * n_heads + idx) * D;
+      g = gq;
+    } else if (idx < n_heads + n_kv_heads) {
+      const uint32_t h = idx - n_heads;
+      src = k_raw + (size_t)tok * kv_row + (size_t)h * D;
+      dst = kcache + (size_t)pos * kv_row + (size_t)h * D;
+      g = gk;
+    } else {
+      const uint32_t h = idx - n_heads - n_kv_heads;
+      src = v_raw + (size_t)tok * kv_row + (size_t)h * D;
+      dst = vcache + (size_t)pos * kv_row + (size_t)h * D;
+    }
+    float e0 = src[lane];
+    float e1 = D == 128 ? src[lane + 64] : 0.f;
+    if (g != nullptr) {  // uniform per wave
+      head_rmsnorm<D>(e0, e1, g[lane], D == 128 ? g[lane + 64] : 0.f, eps);
+      head_rope<D>(e0, e1, s_cs, pairing, lane);
+    }
+    dst[lane] = e0;
+    if (D == 128) dst[lane + 64] = e1;
   }
-  float e0 = lane < D ? src[lane] : 0.f;
-  float e1 = D == 128 ? src[lane + 64] : 0.f;
-  if (g != nullptr) {  // uniform per wave
-    head_rmsnorm<D>(e0, e1, g, lane, eps);
-    head_rope<D>(e0, e1, inv_freq, (int)pos, pairing, lane);
-  }
-  if (lane < D) dst[lane] = e0;
-  if (D == 128) dst[lane + 64] = e1;
 }
 
 hipError_t launch_qk_prologue(const float* q_raw, const float* k_raw, const float* v_raw,
@@ -136,16 +145,14 @@ hipError_t launch_qk_prologue(const float* q_raw, const float* k_raw, const floa
                               int32_t pairing, float* qn_out, float* kcache, float* vcache,
                               uint32_t n_tokens, uint32_t pos0, uint32_t n_heads,
                               uint32_t n_kv_heads, uint32_t head_dim, hipStream_t st) {
-  const uint64_t vecs = (uint64_t)n_tokens * (n_heads + 2 * n_kv_heads);
-  const uint32_t blocks = (uint32_t)((vecs + 3) / 4);
   if (head_dim == 128)
-    hipLaunchKernelGGL(qk_prologue_kernel<128>, dim3(blocks), dim3(256), 0, st, q_raw, k_raw,
-                       v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache, vcache, n_tokens,
-                       pos0, n_heads, n_kv_heads);
+    hipLaunchKernelGGL(qk_prologue_kernel<128>, dim3(n_tokens), dim3(kPrologueThreads), 0, st,
+                       q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
+                       vcache, pos0, n_heads, n_kv_heads);
   else
-    hipLaunchKernelGGL(qk_prologue_kernel<64>, dim3(blocks), dim3(256), 0, st, q_raw, k_raw,
-                       v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache, vcache, n_tokens,
-                       pos0, n_heads, n_kv_heads);
+    hipLaunchKernelGGL(qk_prologue_kernel<64>, dim3(n_tokens), dim3(kPrologueThreads), 0, st,
+                       q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
+                       vcache, pos0, n_heads, n_kv_heads);
   return hipGetLastError();
 }
 
