@@ -341,3 +341,37 @@ def test_decode_ragged_matches_per_sequence_oracle(rng):
         want = oracle.attn(qb, kb, vb, H, Hkv, d, int(lens[b]))
         m = metrics(got[b], want, cf.attention(qb, kb, vb, H, Hkv, d, 1, int(lens[b]) - 1))
         assert meets_bar(m), (b, fmt(m))
+
+
+# ------------------------------------------------------------ golden fixtures --
+def test_golden_fixtures_on_gpu():
+    # tests/golden/golden.npz: seeded inputs with the oracle's outputs and the
+    # float64 closed form; the GPU path through the C ABI must meet the bar on
+    # each, with the prologue's qn and cache rows bit-identical.
+    import os
+    z = np.load(os.path.join(os.path.dirname(__file__), "golden", "golden.npz"))
+    H, Hkv, d = 16, 8, 128
+    got = _decode(z["dec_q"], z["dec_k"], z["dec_v"], H, Hkv, d, 33)
+    m = metrics(got, z["dec_o"], z["dec_o_f64"])
+    assert meets_bar(m), fmt(m)
+    got = _prefill(z["pre_q"], z["pre_k"], z["pre_v"], H, Hkv, d, 13, 5)
+    m = metrics(got, z["pre_o"], z["pre_o_f64"])
+    assert meets_bar(m), fmt(m)
+    # Prologue + prefill of 3 tokens at position 12 onto a 16-row cache.
+    maxk = 16
+    kc = np.zeros(maxk * Hkv * d, np.float32)
+    vc = np.zeros_like(kc)
+    kc[:12 * Hkv * d], vc[:12 * Hkv * d] = z["pro_kc_prefix"], z["pro_vc_prefix"]
+    kcb, vcb, qn, o = dev(kc), dev(vc), empty(3 * H * d), empty(3 * H * d)
+    inv = dev(z["inv_freq"])
+    ops.qk_prologue(dev(z["pro_q"]), dev(z["pro_k"]), dev(z["pro_v"]), dev(z["pro_gq"]),
+                    dev(z["pro_gk"]), inv, EPS, "neox", qn, kcb, vcb, 3, 12, H, Hkv, d, maxk)
+    ws = ops.Workspace(H, Hkv, d, maxk, 3)
+    ops.attn_prefill(qn, kcb, vcb, o, H, Hkv, d, 3, 12, ws)
+    assert np.array_equal(get(qn, 3 * H * d), z["pro_qn"])
+    assert np.array_equal(kcb.download(maxk * Hkv * d)[12 * Hkv * d:15 * Hkv * d], z["pro_kn"])
+    got_o = get(o, 3 * H * d)
+    kfull = kcb.download(maxk * Hkv * d)
+    vfull = vcb.download(maxk * Hkv * d)
+    m = metrics(got_o, z["pro_o"], cf.attention(z["pro_qn"], kfull, vfull, H, Hkv, d, 3, 12))
+    assert meets_bar(m), fmt(m)
