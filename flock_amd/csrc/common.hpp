@@ -173,12 +173,14 @@ hipError_t launch_decode(const float* q, const float* kcache, const float* vcach
                          const DecodeShape& s, const DecodeFused* fused, void* ws, hipStream_t st);
 
 struct PrefillPlan {
-  uint32_t rows_per_tile;   // 128: query-head rows sharing one kv head
+  uint32_t rows_per_tile;   // query-head rows of one work item (all share a kv head)
   uint32_t q_per_tile;      // rows_per_tile / group
   uint32_t n_qtiles;
+  uint32_t paired;          // 1: each workgroup runs q tiles t and n_qtiles-1-t whole
+  uint32_t work_per_kvh;    // workgroups per kv head
   uint32_t ktiles_per_split;
-  uint32_t max_splits;      // splits of the heaviest q-tile
-  uint64_t partial_slots;   // n_qtiles * max_splits * n_kv_heads
+  uint32_t max_splits;      // splits of the heaviest q tile (split mode)
+  uint64_t partial_slots;   // n_qtiles * max_splits * n_kv_heads when splitting
 };
 PrefillPlan prefill_plan(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                          uint32_t n_queries, uint32_t pos0);

@@ -2,12 +2,12 @@
 //
 // The reference (attention_prefill.wgsl:75-175) runs one workgroup per
 // (query, head), streams every key of that query through scalar FMAs and two
-// barrier-heavy tree reductions per 64-key tile. Here one workgroup owns a
-// tile of 128 query-head rows that share one kv head -- (128 / G) queries x
-// the G heads of the group -- so every K/V tile staged in LDS is used by 128
+// barrier-heavy tree reductions per 64-key tile. Here a work item is a "q
+// tile" of 64 query-head rows that share one kv head ((64 / G) queries x the
+// G heads of the group), so every 64-key K/V tile staged in LDS serves 64
 // rows, and both products run on v_mfma_f32_16x16x4f32 (f32 in, f32 out).
 //
-// Per 64-key tile and wave (32 rows = two 16-column blocks):
+// Per 64-key tile, each of the 4 waves owns 16 rows (one 16-column block):
 //   S^T = K Q^T     A = K block [16 keys x 4 dims] from LDS, B = Q^T from
 //                   registers (loaded once); out lane l, reg i holds
 //                   S^T[key 4(l/16)+i][row l%16].
@@ -15,31 +15,38 @@
 //                   same l%16: in-lane max/sum over 16 values, then lane xor
 //                   16 and 32. Running (m, l) per lane, no LDS.
 //   O^T += V^T P^T  B = P^T taken directly from the S^T registers (the key
-//                   order inside a k-step is permuted consistently on both
-//                   operands), A = V^T read from LDS; out lane l, reg j holds
-//                   O^T[channel 4(l/16)+j][row l%16], so the online-softmax
-//                   rescale of O is per lane as well.
-// The d-summation of S uses dim 32*(l/16) + s at step s (any permutation of the
-// summed index is the same dot product), so each lane reads 32 contiguous
-// floats of a K row from LDS.
+//                   order inside a k-step is permuted identically on both
+//                   operands); A = V^T read from LDS. Output row m of channel
+//                   block c is channel CB*m + c (CB = D/16), so a lane reads
+//                   its CB values of a key as contiguous float4s and, at the
+//                   end, holds 4*CB contiguous output channels.
+// The d-summation of S uses dim (D/4)*(l/16) + s at step s (any permutation
+// of the summed index is the same dot product), so each lane reads D/4
+// contiguous floats of a K row from LDS.
 //
-// Causal bound: query at absolute position p sees keys 0..p (the reference's
-// loop bound, attention_prefill.wgsl:90); applied per element.
-// Long rows are split over keys: the grid is (kv head, split, q tile, heaviest
-// tile first); single-split tiles normalise and store o, multi-split tiles
-// store (m, l, acc) partials that prefill_merge_kernel combines.
+// Each tile's K/V rows are loaded into registers while the previous tile is
+// computed, then written to LDS. Causal bound: query at absolute position p
+// sees keys 0..p (attention_prefill.wgsl:90), applied per element.
+//
+// Scheduling (1-D grid, workgroup id = kv head + n_kv_heads * work item, so
+// with 8 kv heads the workgroups of one kv head share an XCD and its L2):
+//   paired: work item w runs q tiles n_qtiles-1-w and w whole (their causal
+//           key counts add up to about the same for every w); writes o.
+//   split:  too few q tiles to fill the GPU (chunked prefill onto a long
+//           cache): work item (q tile, split) runs a range of key tiles and
+//           writes an (m, l, acc) partial that prefill_merge_kernel combines.
 #include "common.hpp"
 
 namespace flk {
 
 typedef float floatx4 __attribute__((ext_vector_type(4)));
 
-constexpr int kRows = 128;   // query-head rows per workgroup
+constexpr int kRows = 64;    // query-head rows per q tile
 constexpr int kBK = 64;      // keys per tile
 constexpr int kPThreads = 256;
-constexpr uint32_t kMinKtPerSplit = 4;
-constexpr uint32_t kTargetItems = 1024;
-constexpr uint64_t kMaxSlots = 2048;
+constexpr uint32_t kMinPairedWG = 192;    // paired mode when it yields this many
+constexpr uint32_t kTargetSplitWG = 256;  // split mode aims at one workgroup per CU
+constexpr uint32_t kMinKtPerSplit = 2;
 
 struct PrefillArgs {
   const float* q;
@@ -51,98 +58,112 @@ struct PrefillArgs {
   uint32_t n_heads, n_kv_heads, group;
   uint32_t n_queries, pos0;
   uint32_t q_per_tile, n_qtiles;
+  uint32_t paired, work_per_kvh;
   uint32_t kt_per_split, max_splits;
   float scale;
 };
 
-__device__ __forceinline__ uint32_t tile_kt(const PrefillArgs& a, uint32_t qt) {
-  const uint32_t q_end = min((qt + 1) * a.q_per_tile, a.n_queries);
-  return (a.pos0 + q_end + kBK - 1) / kBK;
+__host__ __device__ __forceinline__ uint32_t qtile_kt(uint32_t qt, uint32_t q_per_tile,
+                                                      uint32_t n_queries, uint32_t pos0) {
+  const uint32_t q_end = (qt + 1) * q_per_tile < n_queries ? (qt + 1) * q_per_tile : n_queries;
+  return (pos0 + q_end + kBK - 1) / kBK;
 }
 
-__device__ __forceinline__ uint32_t tile_splits(const PrefillArgs& a, uint32_t n_kt) {
-  return (n_kt + a.kt_per_split - 1) / a.kt_per_split;
+__device__ __forceinline__ float4 mask4(float4 v, uint32_t keep) {
+  return make_float4(__uint_as_float(__float_as_uint(v.x) & keep),
+                     __uint_as_float(__float_as_uint(v.y) & keep),
+                     __uint_as_float(__float_as_uint(v.z) & keep),
+                     __uint_as_float(__float_as_uint(v.w) & keep));
 }
 
+// K/V rows of key tile kt into registers: NPF float4 of each per thread.
+// Rows past the last key are loaded from the last key row (a valid address)
+// and zeroed when written to LDS.
+template <int D, int NPF = kBK * D / 4 / kPThreads>
+__device__ __forceinline__ void load_tile(float4 (&pk)[NPF], float4 (&pv)[NPF],
+                                          const PrefillArgs& a, uint32_t kvh, uint32_t kt,
+                                          uint32_t n_keys_total, int tid) {
+  const size_t row = (size_t)a.n_kv_heads * D;
+#pragma unroll
+  for (int i = 0; i < NPF; i++) {
+    const int f = tid + kPThreads * i;
+    const int r = f / (D / 4), c4 = f % (D / 4);
+    const uint32_t key = min(kt * kBK + r, n_keys_total - 1);
+    const size_t off = (size_t)key * row + (size_t)kvh * D + 4 * c4;
+    pk[i] = *reinterpret_cast<const float4*>(a.kcache + off);
+    pv[i] = *reinterpret_cast<const float4*>(a.vcache + off);
+  }
+}
+
+// Runs key tiles [kt0, kt1) for q tile qt of kv head kvh; writes o rows
+// (normalised) when `final`, else the partial of `slot`.
 template <int D>
-__global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
-  constexpr int LDK = D + 4;        // padded LDS row (floats)
-  constexpr int DS = D / 4;         // k-steps of 4 dims
-  constexpr int CHB = D / 16;       // 16-channel blocks of O^T
-  __shared__ __attribute__((aligned(16))) float k_lds[kBK * LDK];
-  __shared__ __attribute__((aligned(16))) float v_lds[kBK * LDK];
+__device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, float* v_lds,
+                                          uint32_t kvh, uint32_t qt, uint32_t kt0, uint32_t kt1,
+                                          bool final, size_t slot) {
+  constexpr int LDK = D + 4;        // padded K row in LDS (floats)
+  constexpr int DS = D / 4;         // k-steps of 4 dims for S
+  constexpr int CB = D / 16;        // channel blocks of O^T
+  constexpr int NPF = kBK * D / 4 / kPThreads;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int lc = lane & 15;   // column within a 16-block
+  const int lc = lane & 15;   // column within the 16-block = row of this lane
   const int lg = lane >> 4;   // lane group 0..3
-
-  const uint32_t kvh = blockIdx.x;
-  const uint32_t split = blockIdx.y;
-  const uint32_t qt = a.n_qtiles - 1 - blockIdx.z;
-  const uint32_t n_kt = tile_kt(a, qt);
-  const uint32_t ns = tile_splits(a, n_kt);
-  if (split >= ns) return;
-  const uint32_t kt0 = split * n_kt / ns;
-  const uint32_t kt1 = (split + 1) * n_kt / ns;
   const uint32_t n_keys_total = a.pos0 + a.n_queries;
-  const size_t row = (size_t)a.n_kv_heads * D;
   const uint32_t q0 = qt * a.q_per_tile;
 
-  // ---- this lane's two columns: row r -> (query, head) ----------------------
-  uint32_t qpos[2];
-  bool col_ok[2];
-  float qreg[2][DS];
-#pragma unroll
-  for (int cb = 0; cb < 2; cb++) {
-    const uint32_t r = wave * 32 + cb * 16 + lc;
-    const uint32_t qi = q0 + r / a.group;
-    const uint32_t h = kvh * a.group + r % a.group;
-    col_ok[cb] = r < a.q_per_tile * a.group && qi < a.n_queries;
-    qpos[cb] = a.pos0 + qi;
+  // ---- this lane's row: r -> (query, head) -----------------------------------
+  const uint32_t r = wave * 16 + lc;
+  const uint32_t qi = q0 + r / a.group;
+  const uint32_t h = kvh * a.group + r % a.group;
+  const bool row_ok = r < a.q_per_tile * a.group && qi < a.n_queries;
+  const uint32_t qpos = a.pos0 + qi;
+
+  float4 pk[NPF], pv[NPF];
+  load_tile<D>(pk, pv, a, kvh, kt0, n_keys_total, tid);
+
+  float qreg[DS];
+  {
     const float4* src = reinterpret_cast<const float4*>(
-        a.q + ((size_t)(col_ok[cb] ? qi : 0) * a.n_heads + h) * D + DS * lg);
+        a.q + ((size_t)(row_ok ? qi : q0) * a.n_heads + (row_ok ? h : kvh * a.group)) * D +
+        DS * lg);
 #pragma unroll
     for (int s4 = 0; s4 < DS / 4; s4++) {
-      const float4 v = col_ok[cb] ? src[s4] : make_float4(0.f, 0.f, 0.f, 0.f);
-      qreg[cb][4 * s4 + 0] = v.x;
-      qreg[cb][4 * s4 + 1] = v.y;
-      qreg[cb][4 * s4 + 2] = v.z;
-      qreg[cb][4 * s4 + 3] = v.w;
+      const float4 v = src[s4];
+      qreg[4 * s4 + 0] = v.x;
+      qreg[4 * s4 + 1] = v.y;
+      qreg[4 * s4 + 2] = v.z;
+      qreg[4 * s4 + 3] = v.w;
     }
   }
 
-  floatx4 oacc[CHB][2];
+  floatx4 oacc[CB];
 #pragma unroll
-  for (int c = 0; c < CHB; c++)
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++) oacc[c][cb] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run[2] = {-INFINITY, -INFINITY};
-  float l_run[2] = {0.f, 0.f};
+  for (int c = 0; c < CB; c++) oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
+  float m_run = -INFINITY, l_run = 0.f;
 
   for (uint32_t kt = kt0; kt < kt1; kt++) {
     const uint32_t key0 = kt * kBK;
-    // ---- stage K and V tiles in LDS ------------------------------------------
-    __syncthreads();  // previous tile fully consumed
+    __syncthreads();  // the previous tile is consumed
 #pragma unroll
-    for (int i = 0; i < (kBK * D / 4) / kPThreads; i++) {
+    for (int i = 0; i < NPF; i++) {
       const int f = tid + kPThreads * i;
-      const int r = f / (D / 4), c4 = f % (D / 4);
-      const uint32_t key = key0 + r;
-      float4 kv = make_float4(0.f, 0.f, 0.f, 0.f), vv = kv;
-      if (key < n_keys_total) {
-        const size_t off = (size_t)key * row + (size_t)kvh * D + 4 * c4;
-        kv = *reinterpret_cast<const float4*>(a.kcache + off);
-        vv = *reinterpret_cast<const float4*>(a.vcache + off);
-      }
-      *reinterpret_cast<float4*>(&k_lds[r * LDK + 4 * c4]) = kv;
-      *reinterpret_cast<float4*>(&v_lds[r * LDK + 4 * c4]) = vv;
+      const int rr = f / (D / 4), c4 = f % (D / 4);
+      // Rows past the last key become zeros (a bit mask, not a select: the
+      // compiler turns a select between two values into a select of their
+      // addresses, which forces the prefetch registers into scratch).
+      const uint32_t keep = key0 + rr < n_keys_total ? 0xffffffffu : 0u;
+      *reinterpret_cast<float4*>(&k_lds[rr * LDK + 4 * c4]) = mask4(pk[i], keep);
+      *reinterpret_cast<float4*>(&v_lds[rr * D + 4 * c4]) = mask4(pv[i], keep);
     }
     __syncthreads();
+    // Next tile's rows (the last tile is simply loaded again at the end).
+    load_tile<D>(pk, pv, a, kvh, kt + 1 < kt1 ? kt + 1 : kt, n_keys_total, tid);
 
     // ---- S^T = K Q^T ------------------------------------------------------------
-    floatx4 sacc[4][2];
+    floatx4 sacc[4];
 #pragma unroll
     for (int kb = 0; kb < 4; kb++) {
       float kf[DS];
@@ -155,113 +176,131 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
         kf[4 * s4 + 2] = v.z;
         kf[4 * s4 + 3] = v.w;
       }
+      floatx4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int cb = 0; cb < 2; cb++) {
-        floatx4 c = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-        for (int s = 0; s < DS; s++) c = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qreg[cb][s], c, 0, 0, 0);
-        sacc[kb][cb] = c;
-      }
+      for (int s = 0; s < DS; s++) c = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qreg[s], c, 0, 0, 0);
+      sacc[kb] = c;
     }
 
-    // ---- online softmax per column ---------------------------------------------
-#pragma unroll
-    for (int cb = 0; cb < 2; cb++) {
-      float mx = -INFINITY;
-#pragma unroll
-      for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const uint32_t key = key0 + kb * 16 + 4 * lg + i;
-          const bool ok = col_ok[cb] && key <= qpos[cb];
-          const float s = ok ? sacc[kb][cb][i] * a.scale : -INFINITY;
-          sacc[kb][cb][i] = s;
-          mx = fmaxf(mx, s);
-        }
-      mx = fmaxf(mx, shfl_xor(mx, 16));
-      mx = fmaxf(mx, shfl_xor(mx, 32));
-      const float mn = fmaxf(m_run[cb], mx);
-      float corr = 1.f, rs = 0.f;
-      if (mn != -INFINITY) {
-        corr = expf(m_run[cb] - mn);
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) {
-            const float p = expf(sacc[kb][cb][i] - mn);
-            sacc[kb][cb][i] = p;
-            rs += p;
-          }
-      } else {
-#pragma unroll
-        for (int kb = 0; kb < 4; kb++)
-#pragma unroll
-          for (int i = 0; i < 4; i++) sacc[kb][cb][i] = 0.f;
-      }
-      rs += shfl_xor(rs, 16);
-      rs += shfl_xor(rs, 32);
-      l_run[cb] = l_run[cb] * corr + rs;
-      m_run[cb] = mn;
-#pragma unroll
-      for (int c = 0; c < CHB; c++) oacc[c][cb] *= corr;
-    }
-
-    // ---- O^T += V^T P^T -------------------------------------------------------
+    // ---- online softmax of this lane's row ------------------------------------
+    float mx = -INFINITY;
 #pragma unroll
     for (int kb = 0; kb < 4; kb++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float* vr = &v_lds[(kb * 16 + 4 * lg + i) * LDK + lc];
+        const uint32_t key = key0 + kb * 16 + 4 * lg + i;
+        const float s = (row_ok && key <= qpos) ? sacc[kb][i] * a.scale : -INFINITY;
+        sacc[kb][i] = s;
+        mx = fmaxf(mx, s);
+      }
+    mx = fmaxf(mx, shfl_xor(mx, 16));
+    mx = fmaxf(mx, shfl_xor(mx, 32));
+    const float mn = fmaxf(m_run, mx);
+    float corr = 1.f, rs = 0.f;
+    if (mn != -INFINITY) {
+      corr = expf(m_run - mn);
 #pragma unroll
-        for (int c = 0; c < CHB; c++) {
-          const float av = vr[16 * c];
+      for (int kb = 0; kb < 4; kb++)
 #pragma unroll
-          for (int cb = 0; cb < 2; cb++)
-            oacc[c][cb] = __builtin_amdgcn_mfma_f32_16x16x4f32(av, sacc[kb][cb][i], oacc[c][cb], 0, 0, 0);
+        for (int i = 0; i < 4; i++) {
+          const float p = expf(sacc[kb][i] - mn);
+          sacc[kb][i] = p;
+          rs += p;
         }
+    } else {
+#pragma unroll
+      for (int kb = 0; kb < 4; kb++) sacc[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+    }
+    rs += shfl_xor(rs, 16);
+    rs += shfl_xor(rs, 32);
+    l_run = l_run * corr + rs;
+    m_run = mn;
+#pragma unroll
+    for (int c = 0; c < CB; c++) oacc[c] *= corr;
+
+    // ---- O^T += V^T P^T ---------------------------------------------------------
+#pragma unroll
+    for (int kb = 0; kb < 4; kb++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float* vr = &v_lds[(kb * 16 + 4 * lg + i) * D + CB * lc];
+        float vv[CB];
+#pragma unroll
+        for (int c4 = 0; c4 < CB / 4; c4++) {
+          const float4 v = *reinterpret_cast<const float4*>(vr + 4 * c4);
+          vv[4 * c4 + 0] = v.x;
+          vv[4 * c4 + 1] = v.y;
+          vv[4 * c4 + 2] = v.z;
+          vv[4 * c4 + 3] = v.w;
+        }
+#pragma unroll
+        for (int c = 0; c < CB; c++)
+          oacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[c], sacc[kb][i], oacc[c], 0, 0, 0);
       }
   }
 
-  // ---- epilogue ------------------------------------------------------------------
-  const bool single = ns == 1;
-  const size_t slot = ((size_t)qt * a.max_splits + split) * a.n_kv_heads + kvh;
+  // ---- epilogue: lane holds channels 4*CB*lg + CB*j + c of its row ------------
+  if (final) {
+    if (!row_ok) return;
+    float* dst = a.o + ((size_t)qi * a.n_heads + h) * D + 4 * CB * lg;
+    const float L = l_run;
 #pragma unroll
-  for (int cb = 0; cb < 2; cb++) {
-    const uint32_t r = wave * 32 + cb * 16 + lc;
-    if (single) {
-      if (!col_ok[cb]) continue;
-      const uint32_t qi = q0 + r / a.group;
-      const uint32_t h = kvh * a.group + r % a.group;
-      float* dst = a.o + ((size_t)qi * a.n_heads + h) * D + 4 * lg;
-      const float L = l_run[cb];
+    for (int j = 0; j < 4; j++)
 #pragma unroll
-      for (int c = 0; c < CHB; c++) {
-        const float4 v = make_float4(oacc[c][cb][0] / L, oacc[c][cb][1] / L, oacc[c][cb][2] / L,
-                                     oacc[c][cb][3] / L);
-        *reinterpret_cast<float4*>(dst + 16 * c) = v;
-      }
-    } else {
-      float* dst = a.part_acc + (slot * kRows + r) * D + 4 * lg;
+      for (int c4 = 0; c4 < CB / 4; c4++)
+        *reinterpret_cast<float4*>(dst + CB * j + 4 * c4) =
+            make_float4(oacc[4 * c4 + 0][j] / L, oacc[4 * c4 + 1][j] / L,
+                        oacc[4 * c4 + 2][j] / L, oacc[4 * c4 + 3][j] / L);
+  } else {
+    float* dst = a.part_acc + (slot * kRows + r) * D + 4 * CB * lg;
 #pragma unroll
-      for (int c = 0; c < CHB; c++)
-        *reinterpret_cast<float4*>(dst + 16 * c) =
-            make_float4(oacc[c][cb][0], oacc[c][cb][1], oacc[c][cb][2], oacc[c][cb][3]);
-      if (lg == 0) a.part_ml[slot * kRows + r] = make_float2(m_run[cb], l_run[cb]);
-    }
+    for (int j = 0; j < 4; j++)
+#pragma unroll
+      for (int c4 = 0; c4 < CB / 4; c4++)
+        *reinterpret_cast<float4*>(dst + CB * j + 4 * c4) =
+            make_float4(oacc[4 * c4 + 0][j], oacc[4 * c4 + 1][j], oacc[4 * c4 + 2][j],
+                        oacc[4 * c4 + 3][j]);
+    if (lg == 0) a.part_ml[slot * kRows + r] = make_float2(m_run, l_run);
   }
 }
 
-// One workgroup per (kv head, q tile, 8 rows); 32 lanes per row (D = 128) or
-// 16 (D = 64), each owning a float4 of channels. Combines the splits of a
-// multi-split tile with log-sum-exp weights; single-split tiles exit.
+template <int D>
+__global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
+  __shared__ __attribute__((aligned(16))) float k_lds[kBK * (D + 4)];
+  __shared__ __attribute__((aligned(16))) float v_lds[kBK * D];
+  const uint32_t kvh = blockIdx.x % a.n_kv_heads;
+  const uint32_t w = blockIdx.x / a.n_kv_heads;
+  if (a.paired) {
+    const uint32_t qt_hi = a.n_qtiles - 1 - w;
+    run_qtile<D>(a, k_lds, v_lds, kvh, qt_hi, 0,
+                 qtile_kt(qt_hi, a.q_per_tile, a.n_queries, a.pos0), true, 0);
+    if (w < qt_hi)
+      run_qtile<D>(a, k_lds, v_lds, kvh, w, 0, qtile_kt(w, a.q_per_tile, a.n_queries, a.pos0),
+                   true, 0);
+    return;
+  }
+  const uint32_t qt = a.n_qtiles - 1 - w / a.max_splits;  // heaviest q tile first
+  const uint32_t split = w % a.max_splits;
+  const uint32_t n_kt = qtile_kt(qt, a.q_per_tile, a.n_queries, a.pos0);
+  const uint32_t ns = (n_kt + a.kt_per_split - 1) / a.kt_per_split;
+  if (split >= ns) return;  // uniform per workgroup
+  const uint32_t kt0 = split * n_kt / ns;
+  const uint32_t kt1 = (split + 1) * n_kt / ns;
+  const size_t slot = ((size_t)qt * a.max_splits + split) * a.n_kv_heads + kvh;
+  run_qtile<D>(a, k_lds, v_lds, kvh, qt, kt0, kt1, ns == 1, slot);
+}
+
+// One workgroup per (kv head, q tile, 256 / (D/4) rows); D/4 lanes per row,
+// each owning a float4 of channels. Combines the splits of a multi-split q
+// tile with log-sum-exp weights; single-split tiles exit.
 template <int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   constexpr int LPR = D / 4;
   constexpr int RPB = 256 / LPR;   // rows per block
   const uint32_t kvh = blockIdx.x;
   const uint32_t qt = blockIdx.y;
-  const uint32_t n_kt = tile_kt(a, qt);
-  const uint32_t ns = tile_splits(a, n_kt);
+  const uint32_t n_kt = qtile_kt(qt, a.q_per_tile, a.n_queries, a.pos0);
+  const uint32_t ns = (n_kt + a.kt_per_split - 1) / a.kt_per_split;
   if (ns == 1) return;
   const uint32_t r = blockIdx.z * RPB + threadIdx.x / LPR;
   const int c = threadIdx.x % LPR;
@@ -300,44 +339,28 @@ PrefillPlan prefill_plan(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_di
   p.rows_per_tile = kRows;
   p.q_per_tile = kRows / group;
   p.n_qtiles = (n_queries + p.q_per_tile - 1) / p.q_per_tile;
-  auto n_kt = [&](uint32_t qt) {
-    const uint32_t q_end = (qt + 1) * p.q_per_tile < n_queries ? (qt + 1) * p.q_per_tile : n_queries;
-    return (pos0 + q_end + kBK - 1) / kBK;
-  };
-  uint64_t total = 0;
-  for (uint32_t qt = 0; qt < p.n_qtiles; qt++) total += n_kt(qt);
-  total *= n_kv_heads;
-  uint64_t ch = (total + kTargetItems - 1) / kTargetItems;
-  if (ch < kMinKtPerSplit) ch = kMinKtPerSplit;
-  const uint32_t max_kt = n_kt(p.n_qtiles - 1);
-  for (;;) {
-    const uint64_t ms = (max_kt + ch - 1) / ch;
-    const uint64_t slots = (uint64_t)p.n_qtiles * ms * n_kv_heads;
-    if (ms <= 1 || slots <= kMaxSlots) {
-      p.ktiles_per_split = (uint32_t)ch;
-      p.max_splits = (uint32_t)ms;
-      p.partial_slots = ms > 1 ? slots : 0;
-      break;
-    }
-    ch++;
+  const uint32_t pairs = (p.n_qtiles + 1) / 2;
+  if ((uint64_t)pairs * n_kv_heads >= kMinPairedWG) {
+    p.paired = 1;
+    p.work_per_kvh = pairs;
+    p.ktiles_per_split = 0;
+    p.max_splits = 1;
+    p.partial_slots = 0;
+    return p;
   }
+  uint64_t total = 0;
+  for (uint32_t qt = 0; qt < p.n_qtiles; qt++) total += qtile_kt(qt, p.q_per_tile, n_queries, pos0);
+  total *= n_kv_heads;
+  uint64_t ch = (total + kTargetSplitWG - 1) / kTargetSplitWG;
+  if (ch < kMinKtPerSplit) ch = kMinKtPerSplit;
+  const uint32_t max_kt = qtile_kt(p.n_qtiles - 1, p.q_per_tile, n_queries, pos0);
+  const uint64_t ms = (max_kt + ch - 1) / ch;
+  p.paired = 0;
+  p.ktiles_per_split = (uint32_t)ch;
+  p.max_splits = (uint32_t)ms;
+  p.work_per_kvh = p.n_qtiles * p.max_splits;
+  p.partial_slots = ms > 1 ? (uint64_t)p.n_qtiles * ms * n_kv_heads : 0;
   return p;
-}
-
-// Upper bound over every plan with n_queries <= max_queries and pos0 +
-// n_queries <= max_keys: splits per tile never exceed ceil(kt / kMinKtPerSplit)
-// and the planner never exceeds kMaxSlots when it splits at all.
-uint64_t prefill_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                          uint32_t max_queries, uint32_t max_keys) {
-  const uint32_t q_per_tile = kRows / (n_heads / n_kv_heads);
-  const uint64_t n_qt = (max_queries + q_per_tile - 1) / q_per_tile;
-  const uint64_t max_kt = (max_keys + kBK - 1) / kBK;
-  const uint64_t ms = (max_kt + kMinKtPerSplit - 1) / kMinKtPerSplit;
-  uint64_t slots = ms > 1 ? n_qt * ms * n_kv_heads : 0;
-  if (slots > kMaxSlots) slots = kMaxSlots;
-  PrefillPlan p{};
-  p.partial_slots = slots;
-  return prefill_ws_bytes(p, head_dim);
 }
 
 uint64_t prefill_ws_bytes(const PrefillPlan& p, uint32_t head_dim) {
@@ -346,12 +369,36 @@ uint64_t prefill_ws_bytes(const PrefillPlan& p, uint32_t head_dim) {
          p.partial_slots * kRows * head_dim * sizeof(float);
 }
 
+// Upper bound over every plan with n_queries <= max_queries and pos0 +
+// n_queries <= max_keys. Only split plans have partials, and only while
+// ceil(n_qtiles / 2) * n_kv_heads < kMinPairedWG. In a split plan the last q
+// tile alone gives total >= n_kv_heads * max_kt key tiles, so ch >= n_kv_heads
+// * max_kt / kTargetSplitWG and ms = ceil(max_kt / ch) <= ceil(kTargetSplitWG /
+// n_kv_heads); also ms <= ceil(max_kt / kMinKtPerSplit) with max_kt <=
+// ceil(max_keys / kBK).
+uint64_t prefill_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                          uint32_t max_queries, uint32_t max_keys) {
+  const uint32_t qpt = kRows / (n_heads / n_kv_heads);
+  const uint64_t max_qt = (max_queries + qpt - 1) / qpt;
+  uint64_t nqt = 0;  // most q tiles a split plan can have
+  for (uint64_t t = 1; t <= max_qt && (t + 1) / 2 * n_kv_heads < kMinPairedWG; t++) nqt = t;
+  if (nqt == 0) return 0;
+  const uint64_t max_kt = ((uint64_t)max_keys + kBK - 1) / kBK;
+  const uint64_t by_wg = (kTargetSplitWG + n_kv_heads - 1) / n_kv_heads;
+  const uint64_t by_kt = (max_kt + kMinKtPerSplit - 1) / kMinKtPerSplit;
+  const uint64_t ms = by_wg < by_kt ? by_wg : by_kt;
+  if (ms <= 1) return 0;
+  PrefillPlan p{};
+  p.partial_slots = nqt * ms * n_kv_heads;
+  return prefill_ws_bytes(p, head_dim);
+}
+
 template <int D>
 static hipError_t launch_prefill_d(const PrefillArgs& a, const PrefillPlan& p, hipStream_t st) {
-  const dim3 grid(a.n_kv_heads, p.max_splits, p.n_qtiles);
+  const dim3 grid(a.n_kv_heads * p.work_per_kvh);
   hipLaunchKernelGGL(prefill_kernel<D>, grid, dim3(kPThreads), 0, st, a);
   hipError_t e = hipGetLastError();
-  if (e != hipSuccess || p.max_splits <= 1) return e;
+  if (e != hipSuccess || p.paired || p.max_splits <= 1) return e;
   constexpr int RPB = 256 / (D / 4);
   const dim3 mgrid(a.n_kv_heads, p.n_qtiles, kRows / RPB);
   hipLaunchKernelGGL(prefill_merge_kernel<D>, mgrid, dim3(256), 0, st, a);
@@ -367,8 +414,8 @@ hipError_t launch_prefill(const float* q, const float* kcache, const float* vcac
   a.kcache = kcache;
   a.vcache = vcache;
   a.o = o;
-  char* w = static_cast<char*>(ws);
   if (p.partial_slots > 0) {
+    char* w = static_cast<char*>(ws);
     a.part_ml = reinterpret_cast<float2*>(w);
     a.part_acc = reinterpret_cast<float*>(w + ws_align(p.partial_slots * kRows * sizeof(float2)));
   }
@@ -379,6 +426,8 @@ hipError_t launch_prefill(const float* q, const float* kcache, const float* vcac
   a.pos0 = pos0;
   a.q_per_tile = p.q_per_tile;
   a.n_qtiles = p.n_qtiles;
+  a.paired = p.paired;
+  a.work_per_kvh = p.work_per_kvh;
   a.kt_per_split = p.ktiles_per_split;
   a.max_splits = p.max_splits;
   a.scale = (float)(1.0 / sqrt((double)head_dim));
