@@ -7,7 +7,9 @@
 // G heads of the group), so every 64-key K/V tile staged in LDS serves 64
 // rows, and both products run on v_mfma_f32_16x16x4f32 (f32 in, f32 out).
 //
-// Per 64-key tile, each of the 4 waves owns 16 rows (one 16-column block):
+// Per 64-key tile, each of 8 waves owns 16 rows (one 16-column block) and one
+// half (32 keys) of the tile; the two halves of a row keep separate online-
+// softmax states and are combined through LDS when the q tile is done:
 //   S^T = K Q^T     A = K block [16 keys x 4 dims] from LDS, B = Q^T from
 //                   registers (loaded once); out lane l, reg i holds
 //                   S^T[key 4(l/16)+i][row l%16].
@@ -43,7 +45,8 @@ typedef float floatx4 __attribute__((ext_vector_type(4)));
 
 constexpr int kRows = 64;    // query-head rows per q tile
 constexpr int kBK = 64;      // keys per tile
-constexpr int kPThreads = 256;
+constexpr int kPThreads = 512;  // 8 waves: 4 row blocks x 2 key halves
+constexpr int kHalfKB = 2;      // 16-key blocks per wave per tile
 constexpr uint32_t kMinPairedWG = 192;    // paired mode when it yields this many
 constexpr uint32_t kTargetSplitWG = 256;  // split mode aims at one workgroup per CU
 constexpr uint32_t kMinKtPerSplit = 2;
@@ -109,13 +112,14 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   const int tid = threadIdx.x;
   const int lane = tid & 63;
   const int wave = tid >> 6;
-  const int lc = lane & 15;   // column within the 16-block = row of this lane
-  const int lg = lane >> 4;   // lane group 0..3
+  const int half = wave >> 2;  // which 32 keys of every tile this wave takes
+  const int lc = lane & 15;    // column within the 16-block = row of this lane
+  const int lg = lane >> 4;    // lane group 0..3
   const uint32_t n_keys_total = a.pos0 + a.n_queries;
   const uint32_t q0 = qt * a.q_per_tile;
 
   // ---- this lane's row: r -> (query, head) -----------------------------------
-  const uint32_t r = wave * 16 + lc;
+  const uint32_t r = (wave & 3) * 16 + lc;
   const uint32_t qi = q0 + r / a.group;
   const uint32_t h = kvh * a.group + r % a.group;
   const bool row_ok = r < a.q_per_tile * a.group && qi < a.n_queries;
@@ -163,9 +167,10 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     load_tile<D>(pk, pv, a, kvh, kt + 1 < kt1 ? kt + 1 : kt, n_keys_total, tid);
 
     // ---- S^T = K Q^T ------------------------------------------------------------
-    floatx4 sacc[4];
+    floatx4 sacc[kHalfKB];
 #pragma unroll
-    for (int kb = 0; kb < 4; kb++) {
+    for (int b = 0; b < kHalfKB; b++) {
+      const int kb = half * kHalfKB + b;
       float kf[DS];
       const float* kr = &k_lds[(kb * 16 + lc) * LDK + DS * lg];
 #pragma unroll
@@ -179,18 +184,18 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
       floatx4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
       for (int s = 0; s < DS; s++) c = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qreg[s], c, 0, 0, 0);
-      sacc[kb] = c;
+      sacc[b] = c;
     }
 
     // ---- online softmax of this lane's row ------------------------------------
     float mx = -INFINITY;
 #pragma unroll
-    for (int kb = 0; kb < 4; kb++)
+    for (int b = 0; b < kHalfKB; b++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const uint32_t key = key0 + kb * 16 + 4 * lg + i;
-        const float s = (row_ok && key <= qpos) ? sacc[kb][i] * a.scale : -INFINITY;
-        sacc[kb][i] = s;
+        const uint32_t key = key0 + (half * kHalfKB + b) * 16 + 4 * lg + i;
+        const float s = (row_ok && key <= qpos) ? sacc[b][i] * a.scale : -INFINITY;
+        sacc[b][i] = s;
         mx = fmaxf(mx, s);
       }
     mx = fmaxf(mx, shfl_xor(mx, 16));
@@ -200,16 +205,16 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     if (mn != -INFINITY) {
       corr = expf(m_run - mn);
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++)
+      for (int b = 0; b < kHalfKB; b++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const float p = expf(sacc[kb][i] - mn);
-          sacc[kb][i] = p;
+          const float p = expf(sacc[b][i] - mn);
+          sacc[b][i] = p;
           rs += p;
         }
     } else {
 #pragma unroll
-      for (int kb = 0; kb < 4; kb++) sacc[kb] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int b = 0; b < kHalfKB; b++) sacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
     rs += shfl_xor(rs, 16);
     rs += shfl_xor(rs, 32);
@@ -220,10 +225,10 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
 
     // ---- O^T += V^T P^T ---------------------------------------------------------
 #pragma unroll
-    for (int kb = 0; kb < 4; kb++)
+    for (int b = 0; b < kHalfKB; b++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float* vr = &v_lds[(kb * 16 + 4 * lg + i) * D + CB * lc];
+        const float* vr = &v_lds[((half * kHalfKB + b) * 16 + 4 * lg + i) * D + CB * lc];
         float vv[CB];
 #pragma unroll
         for (int c4 = 0; c4 < CB / 4; c4++) {
@@ -235,24 +240,19 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
         }
 #pragma unroll
         for (int c = 0; c < CB; c++)
-          oacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[c], sacc[kb][i], oacc[c], 0, 0, 0);
+          oacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[c], sacc[b][i], oacc[c], 0, 0, 0);
       }
   }
 
-  // ---- epilogue: lane holds channels 4*CB*lg + CB*j + c of its row ------------
-  if (final) {
-    if (!row_ok) return;
-    float* dst = a.o + ((size_t)qi * a.n_heads + h) * D + 4 * CB * lg;
-    const float L = l_run;
-#pragma unroll
-    for (int j = 0; j < 4; j++)
-#pragma unroll
-      for (int c4 = 0; c4 < CB / 4; c4++)
-        *reinterpret_cast<float4*>(dst + CB * j + 4 * c4) =
-            make_float4(oacc[4 * c4 + 0][j] / L, oacc[4 * c4 + 1][j] / L,
-                        oacc[4 * c4 + 2][j] / L, oacc[4 * c4 + 3][j] / L);
-  } else {
-    float* dst = a.part_acc + (slot * kRows + r) * D + 4 * CB * lg;
+  // ---- combine the two key halves of each row through LDS --------------------
+  // Lane holds channels 4*CB*lg + CB*j + c of its row. The upper waves park
+  // their (m, l, acc) in the (now free) K tile buffer; the lower waves fold
+  // them in and write the row.
+  __syncthreads();  // every wave is done with the last tile
+  float* m_lds = k_lds;                 // [kRows] m, then [kRows] l
+  float* o_lds = k_lds + 2 * kRows;     // [kRows][D]
+  if (half == 1) {
+    float* dst = o_lds + r * D + 4 * CB * lg;
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
@@ -260,8 +260,39 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
         *reinterpret_cast<float4*>(dst + CB * j + 4 * c4) =
             make_float4(oacc[4 * c4 + 0][j], oacc[4 * c4 + 1][j], oacc[4 * c4 + 2][j],
                         oacc[4 * c4 + 3][j]);
-    if (lg == 0) a.part_ml[slot * kRows + r] = make_float2(m_run, l_run);
+    if (lg == 0) {
+      m_lds[r] = m_run;
+      m_lds[kRows + r] = l_run;
+    }
   }
+  __syncthreads();
+  if (half == 1) return;
+  const float m2 = m_lds[r], l2 = m_lds[kRows + r];
+  const float M = fmaxf(m_run, m2);
+  const float w1 = m_run == -INFINITY ? 0.f : expf(m_run - M);
+  const float w2 = m2 == -INFINITY ? 0.f : expf(m2 - M);
+  const float L = l_run * w1 + l2 * w2;
+  const float* o2 = o_lds + r * D + 4 * CB * lg;
+  float* dst;
+  if (final) {
+    if (!row_ok) return;
+    dst = a.o + ((size_t)qi * a.n_heads + h) * D + 4 * CB * lg;
+  } else {
+    dst = a.part_acc + (slot * kRows + r) * D + 4 * CB * lg;
+    if (lg == 0) a.part_ml[slot * kRows + r] = make_float2(M, L);
+  }
+#pragma unroll
+  for (int j = 0; j < 4; j++)
+#pragma unroll
+    for (int c4 = 0; c4 < CB / 4; c4++) {
+      const float4 p = *reinterpret_cast<const float4*>(o2 + CB * j + 4 * c4);
+      float4 v = make_float4(oacc[4 * c4 + 0][j] * w1 + p.x * w2,
+                             oacc[4 * c4 + 1][j] * w1 + p.y * w2,
+                             oacc[4 * c4 + 2][j] * w1 + p.z * w2,
+                             oacc[4 * c4 + 3][j] * w1 + p.w * w2);
+      if (final) v = make_float4(v.x / L, v.y / L, v.z / L, v.w / L);
+      *reinterpret_cast<float4*>(dst + CB * j + 4 * c4) = v;
+    }
 }
 
 template <int D>
