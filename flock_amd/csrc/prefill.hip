@@ -98,6 +98,24 @@ __device__ __forceinline__ void load_tile(float4 (&pk)[NPF], float4 (&pv)[NPF],
   }
 }
 
+// Registers of key tile kt into one LDS buffer (K rows padded to D + 4).
+// Rows past the last key become zeros (a bit mask, not a select: the compiler
+// turns a select between two values into a select of their addresses, which
+// forces the prefetch registers into scratch).
+template <int D, int NPF = kBK * D / 4 / kPThreads>
+__device__ __forceinline__ void store_tile(const float4 (&pk)[NPF], const float4 (&pv)[NPF],
+                                           float* k_lds, float* v_lds, uint32_t kt,
+                                           uint32_t n_keys_total, int tid) {
+#pragma unroll
+  for (int i = 0; i < NPF; i++) {
+    const int f = tid + kPThreads * i;
+    const int rr = f / (D / 4), c4 = f % (D / 4);
+    const uint32_t keep = kt * kBK + rr < n_keys_total ? 0xffffffffu : 0u;
+    *reinterpret_cast<float4*>(&k_lds[rr * (D + 4) + 4 * c4]) = mask4(pk[i], keep);
+    *reinterpret_cast<float4*>(&v_lds[rr * D + 4 * c4]) = mask4(pv[i], keep);
+  }
+}
+
 // Runs key tiles [kt0, kt1) for q tile qt of kv head kvh; writes o rows
 // (normalised) when `final`, else the partial of `slot`.
 template <int D>
@@ -115,6 +133,12 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   const int half = wave >> 2;  // which 32 keys of every tile this wave takes
   const int lc = lane & 15;    // column within the 16-block = row of this lane
   const int lg = lane >> 4;    // lane group 0..3
+  // V-read swizzle (D = 128): A-operand lane lc supplies channel 8*lc + (c ^
+  // 4*sw_rd) of block c, so output row m of the O^T accumulators holds channel
+  // 8*m + (c ^ 4*((m >> 3) & 1)); for this lane's rows m = 4*lg + j that bit
+  // is sw_wr.
+  const int sw_rd = CB == 8 ? (lc >> 3) & 1 : 0;
+  const int sw_wr = CB == 8 ? (lg >> 1) & 1 : 0;
   const uint32_t n_keys_total = a.pos0 + a.n_queries;
   const uint32_t q0 = qt * a.q_per_tile;
 
@@ -148,23 +172,25 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   for (int c = 0; c < CB; c++) oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
+  // Two LDS buffers: tile kt is computed from buffer (kt - kt0) & 1 while
+  // tile kt + 1 is stored into the other one and tile kt + 2 loads into
+  // registers; one barrier per tile separates the two.
+  __syncthreads();  // LDS may still hold the previous q tile's merge data
+  store_tile<D>(pk, pv, k_lds, v_lds, kt0, n_keys_total, tid);
+  load_tile<D>(pk, pv, a, kvh, kt0 + 1 < kt1 ? kt0 + 1 : kt0, n_keys_total, tid);
+  __syncthreads();
+
   for (uint32_t kt = kt0; kt < kt1; kt++) {
     const uint32_t key0 = kt * kBK;
-    __syncthreads();  // the previous tile is consumed
-#pragma unroll
-    for (int i = 0; i < NPF; i++) {
-      const int f = tid + kPThreads * i;
-      const int rr = f / (D / 4), c4 = f % (D / 4);
-      // Rows past the last key become zeros (a bit mask, not a select: the
-      // compiler turns a select between two values into a select of their
-      // addresses, which forces the prefetch registers into scratch).
-      const uint32_t keep = key0 + rr < n_keys_total ? 0xffffffffu : 0u;
-      *reinterpret_cast<float4*>(&k_lds[rr * LDK + 4 * c4]) = mask4(pk[i], keep);
-      *reinterpret_cast<float4*>(&v_lds[rr * D + 4 * c4]) = mask4(pv[i], keep);
+    const int buf = (kt - kt0) & 1;
+    const float* kt_lds = k_lds + buf * (kBK * LDK);
+    const float* vt_lds = v_lds + buf * (kBK * D);
+    if (kt + 1 < kt1) {
+      store_tile<D>(pk, pv, k_lds + (buf ^ 1) * (kBK * LDK), v_lds + (buf ^ 1) * (kBK * D),
+                    kt + 1, n_keys_total, tid);
+      // The tile after (the last one is simply loaded again at the end).
+      load_tile<D>(pk, pv, a, kvh, kt + 2 < kt1 ? kt + 2 : kt + 1, n_keys_total, tid);
     }
-    __syncthreads();
-    // Next tile's rows (the last tile is simply loaded again at the end).
-    load_tile<D>(pk, pv, a, kvh, kt + 1 < kt1 ? kt + 1 : kt, n_keys_total, tid);
 
     // ---- S^T = K Q^T ------------------------------------------------------------
     floatx4 sacc[kHalfKB];
@@ -172,7 +198,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     for (int b = 0; b < kHalfKB; b++) {
       const int kb = half * kHalfKB + b;
       float kf[DS];
-      const float* kr = &k_lds[(kb * 16 + lc) * LDK + DS * lg];
+      const float* kr = &kt_lds[(kb * 16 + lc) * LDK + DS * lg];
 #pragma unroll
       for (int s4 = 0; s4 < DS / 4; s4++) {
         const float4 v = *reinterpret_cast<const float4*>(kr + 4 * s4);
@@ -228,11 +254,13 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     for (int b = 0; b < kHalfKB; b++)
 #pragma unroll
       for (int i = 0; i < 4; i++) {
-        const float* vr = &v_lds[((half * kHalfKB + b) * 16 + 4 * lg + i) * D + CB * lc];
+        const float* vr = &vt_lds[((half * kHalfKB + b) * 16 + 4 * lg + i) * D + CB * lc];
         float vv[CB];
 #pragma unroll
         for (int c4 = 0; c4 < CB / 4; c4++) {
-          const float4 v = *reinterpret_cast<const float4*>(vr + 4 * c4);
+          // Lanes 8..15 of a row group read their two float4s in the other
+          // order, so the 16 lanes hit 16 distinct 16-byte bank slots.
+          const float4 v = *reinterpret_cast<const float4*>(vr + 4 * (c4 ^ sw_rd));
           vv[4 * c4 + 0] = v.x;
           vv[4 * c4 + 1] = v.y;
           vv[4 * c4 + 2] = v.z;
@@ -242,14 +270,14 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
         for (int c = 0; c < CB; c++)
           oacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[c], sacc[b][i], oacc[c], 0, 0, 0);
       }
+    __syncthreads();  // tile kt + 1 stored; buffer of tile kt free again
   }
 
   // ---- combine the two key halves of each row through LDS --------------------
   // Lane holds channels 4*CB*lg + CB*j + c of its row. The upper waves park
   // their (m, l, acc) in the (now free) K tile buffer; the lower waves fold
   // them in and write the row.
-  __syncthreads();  // every wave is done with the last tile
-  float* m_lds = k_lds;                 // [kRows] m, then [kRows] l
+  float* m_lds = k_lds;  // every wave passed the last tile's barrier                 // [kRows] m, then [kRows] l
   float* o_lds = k_lds + 2 * kRows;     // [kRows][D]
   if (half == 1) {
     float* dst = o_lds + r * D + 4 * CB * lg;
@@ -257,7 +285,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     for (int j = 0; j < 4; j++)
 #pragma unroll
       for (int c4 = 0; c4 < CB / 4; c4++)
-        *reinterpret_cast<float4*>(dst + CB * j + 4 * c4) =
+        *reinterpret_cast<float4*>(dst + CB * j + 4 * (c4 ^ sw_wr)) =
             make_float4(oacc[4 * c4 + 0][j], oacc[4 * c4 + 1][j], oacc[4 * c4 + 2][j],
                         oacc[4 * c4 + 3][j]);
     if (lg == 0) {
@@ -285,20 +313,20 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   for (int j = 0; j < 4; j++)
 #pragma unroll
     for (int c4 = 0; c4 < CB / 4; c4++) {
-      const float4 p = *reinterpret_cast<const float4*>(o2 + CB * j + 4 * c4);
+      const float4 p = *reinterpret_cast<const float4*>(o2 + CB * j + 4 * (c4 ^ sw_wr));
       float4 v = make_float4(oacc[4 * c4 + 0][j] * w1 + p.x * w2,
                              oacc[4 * c4 + 1][j] * w1 + p.y * w2,
                              oacc[4 * c4 + 2][j] * w1 + p.z * w2,
                              oacc[4 * c4 + 3][j] * w1 + p.w * w2);
       if (final) v = make_float4(v.x / L, v.y / L, v.z / L, v.w / L);
-      *reinterpret_cast<float4*>(dst + CB * j + 4 * c4) = v;
+      *reinterpret_cast<float4*>(dst + CB * j + 4 * (c4 ^ sw_wr)) = v;
     }
 }
 
 template <int D>
 __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) float k_lds[kBK * (D + 4)];
-  __shared__ __attribute__((aligned(16))) float v_lds[kBK * D];
+  __shared__ __attribute__((aligned(16))) float k_lds[2 * kBK * (D + 4)];
+  __shared__ __attribute__((aligned(16))) float v_lds[2 * kBK * D];
   const uint32_t kvh = blockIdx.x % a.n_kv_heads;
   const uint32_t w = blockIdx.x / a.n_kv_heads;
   if (a.paired) {
