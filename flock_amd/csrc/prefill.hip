@@ -63,7 +63,7 @@ struct PrefillArgs {
   uint32_t q_per_tile, n_qtiles;
   uint32_t paired, work_per_kvh;
   uint32_t kt_per_split, max_splits;
-  float scale;
+  float scale_log2e;  // fr(1/sqrt(d) * log2(e)): scores in base-2 units
 };
 
 __host__ __device__ __forceinline__ uint32_t qtile_kt(uint32_t qt, uint32_t q_per_tile,
@@ -172,6 +172,11 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   for (int c = 0; c < CB; c++) oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
   float m_run = -INFINITY, l_run = 0.f;
 
+  // A tile needs no causal mask when its last key is at or before the q
+  // tile's first query position and every row of the q tile is live.
+  const bool all_rows = a.q_per_tile * a.group == kRows && q0 + a.q_per_tile <= a.n_queries;
+  auto full_tile = [&](uint32_t key0) { return all_rows && key0 + kBK - 1 <= a.pos0 + q0; };
+
   // Two LDS buffers: tile kt is computed from buffer (kt - kt0) & 1 while
   // tile kt + 1 is stored into the other one and tile kt + 2 loads into
   // registers; one barrier per tile separates the two.
@@ -213,28 +218,42 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
       sacc[b] = c;
     }
 
-    // ---- online softmax of this lane's row ------------------------------------
+    // ---- online softmax of this lane's row (base 2) ----------------------------
+    // Scores are kept as log2-scaled values t = (q.k) * scale * log2(e), so
+    // every exponential is one v_exp_f32; m_run is in the same units. Tiles
+    // wholly below the causal diagonal with every row live skip the mask.
     float mx = -INFINITY;
+    if (full_tile(key0)) {
 #pragma unroll
-    for (int b = 0; b < kHalfKB; b++)
+      for (int b = 0; b < kHalfKB; b++)
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const uint32_t key = key0 + (half * kHalfKB + b) * 16 + 4 * lg + i;
-        const float s = (row_ok && key <= qpos) ? sacc[b][i] * a.scale : -INFINITY;
-        sacc[b][i] = s;
-        mx = fmaxf(mx, s);
-      }
+        for (int i = 0; i < 4; i++) {
+          const float t = sacc[b][i] * a.scale_log2e;
+          sacc[b][i] = t;
+          mx = fmaxf(mx, t);
+        }
+    } else {
+#pragma unroll
+      for (int b = 0; b < kHalfKB; b++)
+#pragma unroll
+        for (int i = 0; i < 4; i++) {
+          const uint32_t key = key0 + (half * kHalfKB + b) * 16 + 4 * lg + i;
+          const float t = (row_ok && key <= qpos) ? sacc[b][i] * a.scale_log2e : -INFINITY;
+          sacc[b][i] = t;
+          mx = fmaxf(mx, t);
+        }
+    }
     mx = fmaxf(mx, shfl_xor(mx, 16));
     mx = fmaxf(mx, shfl_xor(mx, 32));
     const float mn = fmaxf(m_run, mx);
     float corr = 1.f, rs = 0.f;
     if (mn != -INFINITY) {
-      corr = expf(m_run - mn);
+      corr = __builtin_amdgcn_exp2f(m_run - mn);
 #pragma unroll
       for (int b = 0; b < kHalfKB; b++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
-          const float p = expf(sacc[b][i] - mn);
+          const float p = __builtin_amdgcn_exp2f(sacc[b][i] - mn);
           sacc[b][i] = p;
           rs += p;
         }
@@ -297,8 +316,8 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   if (half == 1) return;
   const float m2 = m_lds[r], l2 = m_lds[kRows + r];
   const float M = fmaxf(m_run, m2);
-  const float w1 = m_run == -INFINITY ? 0.f : expf(m_run - M);
-  const float w2 = m2 == -INFINITY ? 0.f : expf(m2 - M);
+  const float w1 = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - M);
+  const float w2 = m2 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m2 - M);
   const float L = l_run * w1 + l2 * w2;
   const float* o2 = o_lds + r * D + 4 * CB * lg;
   float* dst;
@@ -377,7 +396,7 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
     const size_t slot = ((size_t)qt * a.max_splits + s) * a.n_kv_heads + kvh;
     const float2 ml = a.part_ml[slot * kRows + r];
     if (ml.x == -INFINITY) continue;
-    const float w = expf(ml.x - M);
+    const float w = __builtin_amdgcn_exp2f(ml.x - M);  // m is in log2 units
     const float4 p = reinterpret_cast<const float4*>(a.part_acc + (slot * kRows + r) * D)[c];
     L = fmaf(ml.y, w, L);
     A.x = fmaf(p.x, w, A.x);
@@ -489,7 +508,7 @@ hipError_t launch_prefill(const float* q, const float* kcache, const float* vcac
   a.work_per_kvh = p.work_per_kvh;
   a.kt_per_split = p.ktiles_per_split;
   a.max_splits = p.max_splits;
-  a.scale = (float)(1.0 / sqrt((double)head_dim));
+  a.scale_log2e = (float)(1.4426950408889634 / sqrt((double)head_dim));
   if (head_dim == 128) return launch_prefill_d<128>(a, p, st);
   return launch_prefill_d<64>(a, p, st);
 }
