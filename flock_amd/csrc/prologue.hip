@@ -111,10 +111,9 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
 
   const uint32_t per_tok = n_heads + 2 * n_kv_heads;
   const size_t kv_row = (size_t)n_kv_heads * D;
-  for (uint32_t idx = wave; idx < per_tok; idx += kPrologueThreads / 64) {
-    const float* src;
-    float* dst;
-    const float* g = nullptr;
+  // Vector idx -> (source, destination, gain): q heads, then k heads, then v.
+  auto locate = [&](uint32_t idx, const float*& src, float*& dst, const float*& g) {
+    g = nullptr;
     if (idx < n_heads) {
       src = q_raw + ((size_t)tok * n_heads + idx) * D;
       dst = qn_out + ((size_t)tok * n_heads + idx) * D;
@@ -129,14 +128,42 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
       src = v_raw + (size_t)tok * kv_row + (size_t)h * D;
       dst = vcache + (size_t)pos * kv_row + (size_t)h * D;
     }
-    float e0 = src[lane];
-    float e1 = D == 128 ? src[lane + 64] : 0.f;
-    if (g != nullptr) {  // uniform per wave
-      head_rmsnorm<D>(e0, e1, g[lane], D == 128 ? g[lane + 64] : 0.f, eps);
-      head_rope<D>(e0, e1, s_cs, pairing, lane);
+  };
+  const float gq0 = gq[lane], gq1 = D == 128 ? gq[lane + 64] : 0.f;
+  const float gk0 = gk[lane], gk1 = D == 128 ? gk[lane + 64] : 0.f;
+  // Each wave takes vectors wave, wave + 4, ...; a batch of kBatch vectors is
+  // loaded before any is used, so their memory latency overlaps.
+  constexpr int kWaves = kPrologueThreads / 64;
+  constexpr int kBatch = 8;
+  for (uint32_t base = wave; base < per_tok; base += kWaves * kBatch) {
+    float e0[kBatch], e1[kBatch];
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const uint32_t idx = min(base + kWaves * b, per_tok - 1);  // extras reload the last
+      const float* src;
+      float* dst;
+      const float* g;
+      locate(idx, src, dst, g);
+      e0[b] = src[lane];
+      e1[b] = D == 128 ? src[lane + 64] : 0.f;
     }
-    dst[lane] = e0;
-    if (D == 128) dst[lane + 64] = e1;
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      const uint32_t idx = base + kWaves * b;
+      if (idx >= per_tok) continue;  // uniform per wave
+      const float* src;
+      float* dst;
+      const float* g;
+      locate(idx, src, dst, g);
+      float x0 = e0[b], x1 = e1[b];
+      if (g != nullptr) {  // uniform per wave
+        const bool is_q = idx < n_heads;
+        head_rmsnorm<D>(x0, x1, is_q ? gq0 : gk0, is_q ? gq1 : gk1, eps);
+        head_rope<D>(x0, x1, s_cs, pairing, lane);
+      }
+      dst[lane] = x0;
+      if (D == 128) dst[lane + 64] = x1;
+    }
   }
 }
 
