@@ -165,7 +165,6 @@ struct DecodeShape {
   uint32_t max_n_keys;  // n_keys for a single sequence
 };
 
-uint32_t decode_keys_per_split(const DecodeShape& s);
 uint64_t decode_ws_bytes(const DecodeShape& s);
 uint64_t decode_ws_bound(const DecodeShape& s);
 hipError_t launch_decode(const float* q, const float* kcache, const float* vcache, float* o,

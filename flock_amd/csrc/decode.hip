@@ -47,8 +47,9 @@ struct DecodeArgs {
   const uint32_t* n_keys_dev;   // ragged only
   uint32_t n_keys;              // single sequence (ragged: the bound max_n_keys)
   uint32_t n_heads, n_kv_heads;
-  uint32_t kps;                 // keys per split
-  uint32_t max_splits;
+  uint32_t kpi;                 // keys per block (one loop iteration of a slot group)
+  uint32_t bps;                 // blocks per split (a sequence's split count divisor)
+  uint32_t max_splits;          // cap on splits per sequence (= grid y)
   float scale;
   float2* part_ml;              // [seq][head][split] (m, l)
   float* part_acc;              // [seq][head][split][D]
@@ -73,8 +74,11 @@ struct DecodeArgs {
 #ifndef FLK_DECODE_RAGGED_TARGET_WG
 #define FLK_DECODE_RAGGED_TARGET_WG 1024
 #endif
+#ifndef FLK_DECODE_NT
+#define FLK_DECODE_NT 1  // K/V rows are read with the non-temporal hint (0: plain loads)
+#endif
 #ifndef FLK_DECODE_UNROLL
-#define FLK_DECODE_UNROLL 8
+#define FLK_DECODE_UNROLL 4
 #endif
 constexpr int kDecodeThreads = 256;
 constexpr int kMergeThreads = 256;
@@ -84,6 +88,13 @@ constexpr int kMergeBatch = 8;   // splits per thread per round of loads
 // Keys per slot per iteration: fewer when G is large, to bound registers.
 __host__ __device__ constexpr int decode_unroll(int G) {
   return G <= 2 ? FLK_DECODE_UNROLL : (G <= 4 ? 4 : 2);
+}
+
+// Splits of a sequence with n_keys keys: ceil(blocks / bps), at most
+// max_splits. Both launches evaluate it identically.
+__device__ __forceinline__ uint32_t seq_splits(const DecodeArgs& a, uint32_t n_keys) {
+  const uint32_t nb = (n_keys + a.kpi - 1) / a.kpi;
+  return min(a.max_splits, (nb + a.bps - 1) / a.bps);
 }
 
 // Keys sequence `seq` attends: the argument for one sequence; for a ragged
@@ -103,8 +114,16 @@ __device__ __forceinline__ void load_keys(float4 (&kr)[U], float4 (&vr)[U], cons
 #pragma unroll
   for (int u = 0; u < U; u++) {
     const uint32_t t = min(base + u * PH + ph, t1 - 1);
+#if FLK_DECODE_NT
+    typedef float f4v __attribute__((ext_vector_type(4)));
+    const f4v k4 = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(kb + (size_t)t * row4));
+    const f4v v4 = __builtin_nontemporal_load(reinterpret_cast<const f4v*>(vb + (size_t)t * row4));
+    kr[u] = make_float4(k4.x, k4.y, k4.z, k4.w);
+    vr[u] = make_float4(v4.x, v4.y, v4.z, v4.w);
+#else
     kr[u] = kb[(size_t)t * row4];
     vr[u] = vb[(size_t)t * row4];
+#endif
   }
 }
 
@@ -201,7 +220,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs
         a.o[((size_t)seq * a.n_heads + h0) * D + i] = 0.f;
     return;
   }
-  const uint32_t n_splits = (n_keys + a.kps - 1) / a.kps;
+  const uint32_t n_splits = seq_splits(a, n_keys);
   if (split >= n_splits) return;  // uniform per workgroup
   // Blocks of KPI keys are dealt round-robin: split s takes blocks s, s +
   // n_splits, ..., so at any time the workgroups of a launch read neighbouring
@@ -398,7 +417,7 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs 
   const uint32_t head = blockIdx.x;
   const uint32_t seq = blockIdx.z;
   const uint32_t n_keys = seq_keys(a, seq);
-  const uint32_t n_splits = (n_keys + a.kps - 1) / a.kps;
+  const uint32_t n_splits = seq_splits(a, n_keys);
   if (n_splits <= 1) return;  // written by the split kernel (or empty)
   const int tid = threadIdx.x;
   const int grp = tid / kMergeCols;
@@ -408,19 +427,19 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs 
   float M = -INFINITY, L = 0.f;
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
   for (uint32_t s0 = grp; s0 < n_splits; s0 += GROUPS * kMergeBatch) {
+    // Unconditional loads (indices past the last split reload it and are
+    // given weight 0), so the wait counts stay exact.
     float2 ml[kMergeBatch];
     float4 pa[kMergeBatch];
 #pragma unroll
     for (int i = 0; i < kMergeBatch; i++) {
-      const uint32_t s = s0 + GROUPS * i;
-      if (s < n_splits) {
-        ml[i] = a.part_ml[p0 + s];
-        pa[i] = reinterpret_cast<const float4*>(a.part_acc + (p0 + s) * D)[c];
-      } else {
-        ml[i] = make_float2(-INFINITY, 0.f);
-        pa[i] = make_float4(0.f, 0.f, 0.f, 0.f);
-      }
+      const uint32_t s = min(s0 + GROUPS * i, n_splits - 1);
+      ml[i] = a.part_ml[p0 + s];
+      pa[i] = reinterpret_cast<const float4*>(a.part_acc + (p0 + s) * D)[c];
     }
+#pragma unroll
+    for (int i = 0; i < kMergeBatch; i++)
+      if (s0 + GROUPS * i >= n_splits) ml[i].x = -INFINITY;
     float mx = M;
 #pragma unroll
     for (int i = 0; i < kMergeBatch; i++) mx = fmaxf(mx, ml[i].x);
@@ -484,26 +503,37 @@ static uint32_t keys_per_iter(const DecodeShape& s) {
   return slots / kv_heads_per_wg(s.n_kv_heads) * U;
 }
 
-// Keys per split: aim for a fixed number of split workgroups in total (one or
-// two per CU stream best; more only queue up), in whole loop iterations and at
-// least four of them. A ragged batch plans from its longest sequence, so it
-// asks for more, shorter splits to keep short sequences from idling CUs.
+// Split plan. A single sequence gets one split workgroup per CU group:
+// kTargetWG / (n_kv_heads / KH) splits (256 for Qwen3: one per CU, each
+// taking every 256th block), fewer when there are under kMinBps blocks per
+// split. A ragged batch plans from its longest sequence: bps blocks per
+// split, chosen so the longest batch of that length would give about
+// kRaggedTargetWG workgroups, and each sequence gets ceil(blocks / bps).
 constexpr uint32_t kTargetWG = FLK_DECODE_TARGET_WG;
 constexpr uint32_t kRaggedTargetWG = FLK_DECODE_RAGGED_TARGET_WG;
+constexpr uint32_t kMinBps = 4;
 
-uint32_t decode_keys_per_split(const DecodeShape& s) {
-  const uint64_t kpi = keys_per_iter(s);
-  const uint64_t units = (uint64_t)(s.n_kv_heads / kv_heads_per_wg(s.n_kv_heads)) * s.n_seqs;
-  const uint64_t target = s.n_seqs > 1 ? kRaggedTargetWG : kTargetWG;
-  uint64_t kps = ((uint64_t)s.max_n_keys * units + target - 1) / target;
-  kps = (kps + kpi - 1) / kpi * kpi;
-  if (kps < 4 * kpi) kps = 4 * kpi;
-  return (uint32_t)kps;
-}
+struct SplitPlan {
+  uint32_t kpi, bps, max_splits;
+};
 
-static uint32_t max_splits_for(const DecodeShape& s) {
-  const uint32_t kps = decode_keys_per_split(s);
-  return (s.max_n_keys + kps - 1) / kps;
+static SplitPlan split_plan(const DecodeShape& s) {
+  SplitPlan p{};
+  p.kpi = keys_per_iter(s);
+  const uint64_t groups = s.n_kv_heads / kv_heads_per_wg(s.n_kv_heads);
+  const uint64_t nb = ((uint64_t)s.max_n_keys + p.kpi - 1) / p.kpi;
+  if (s.n_seqs == 1) {
+    const uint64_t by_wg = kTargetWG / groups > 0 ? kTargetWG / groups : 1;
+    const uint64_t by_len = (nb + kMinBps - 1) / kMinBps;
+    p.bps = kMinBps;
+    p.max_splits = (uint32_t)(by_wg < by_len ? by_wg : by_len);
+  } else {
+    uint64_t bps = (nb * groups * s.n_seqs + kRaggedTargetWG - 1) / kRaggedTargetWG;
+    if (bps < kMinBps) bps = kMinBps;
+    p.bps = (uint32_t)bps;
+    p.max_splits = (uint32_t)((nb + bps - 1) / bps);
+  }
+  return p;
 }
 
 // Partials of `slots` (sequence, head, split) triples.
@@ -512,24 +542,25 @@ static uint64_t ws_for_slots(uint64_t slots, uint32_t head_dim) {
 }
 
 uint64_t decode_ws_bytes(const DecodeShape& s) {
-  const uint32_t splits = max_splits_for(s);
-  if (splits <= 1) return 0;
-  return ws_for_slots((uint64_t)s.n_seqs * s.n_heads * splits, s.head_dim);
+  const SplitPlan p = split_plan(s);
+  if (p.max_splits <= 1) return 0;
+  return ws_for_slots((uint64_t)s.n_seqs * s.n_heads * p.max_splits, s.head_dim);
 }
 
 // Bound over every call with n_keys <= s.max_n_keys and n_seqs <= s.n_seqs
-// (single-sequence calls included). For n sequences kps >= max(4 * kpi,
-// n_keys * units / target), so a sequence has at most min(ceil(max_n_keys /
-// (4 * kpi)), ceil(target / units)) splits; take the largest n * splits.
+// (single-sequence calls included). One sequence: max_splits <= kTargetWG /
+// groups. n > 1 sequences: bps >= nb * groups * n / kRaggedTargetWG, so
+// max_splits = ceil(nb / bps) <= kRaggedTargetWG / (groups * n) + 1; both
+// also <= ceil(nb / kMinBps). Take the largest n * splits.
 uint64_t decode_ws_bound(const DecodeShape& s) {
   const uint64_t kpi = keys_per_iter(s);
-  const uint64_t by_len = (s.max_n_keys + 4 * kpi - 1) / (4 * kpi);
   const uint64_t groups = s.n_kv_heads / kv_heads_per_wg(s.n_kv_heads);
+  const uint64_t nb = ((uint64_t)s.max_n_keys + kpi - 1) / kpi;
+  const uint64_t by_len = (nb + kMinBps - 1) / kMinBps;
   uint64_t best = 0;
   for (uint64_t n = 1; n <= s.n_seqs; n++) {
-    const uint64_t units = groups * n;
-    const uint64_t target = n > 1 ? kRaggedTargetWG : kTargetWG;
-    const uint64_t by_wg = (target + units - 1) / units;
+    const uint64_t by_wg = n == 1 ? (kTargetWG / groups > 0 ? kTargetWG / groups : 1)
+                                  : kRaggedTargetWG / (groups * n) + 1;
     const uint64_t splits = by_len < by_wg ? by_len : by_wg;
     if (splits > 1 && n * splits > best) best = n * splits;
   }
@@ -583,8 +614,10 @@ hipError_t launch_decode(const float* q, const float* kcache, const float* vcach
   a.n_keys = s.max_n_keys;
   a.n_heads = s.n_heads;
   a.n_kv_heads = s.n_kv_heads;
-  a.kps = decode_keys_per_split(s);
-  a.max_splits = max_splits_for(s);
+  const SplitPlan plan = split_plan(s);
+  a.kpi = plan.kpi;
+  a.bps = plan.bps;
+  a.max_splits = plan.max_splits;
   a.scale = (float)(1.0 / sqrt((double)s.head_dim));
   if (a.max_splits > 1) {
     char* w = static_cast<char*>(ws);
