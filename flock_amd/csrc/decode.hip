@@ -5,13 +5,14 @@
 // $MAX_KEYS and leaves the GPU with 16 workgroups. Here two launches:
 //
 // decode_split_kernel<D, G, KH>  grid (n_kv_heads / KH, n_splits, n_seqs),
-//   256 threads. A workgroup streams a share of the keys of KH adjacent kv heads and
+//   512 threads. A workgroup streams a share of the keys of KH adjacent kv heads and
 //   serves the KH * G query heads that read them (G = n_heads / n_kv_heads),
 //   so each K/V byte is read from HBM once. The cache row of one (key, kv head)
-//   is D floats, loaded by D/4 lanes as float4: a "slot". The 256 / (D/4)
+//   is D floats, loaded by D/4 lanes as float4: a "slot". The 512 / (D/4)
 //   slots are KH kv heads x PH key phases; with KH = n_kv_heads (8 for
-//   Qwen3-0.6B) and D = 128 a workgroup reads whole 4 KB cache rows, one key
-//   after another, as one contiguous stream per K and V.
+//   Qwen3-0.6B) and D = 128 a workgroup reads whole 4 KB cache rows, two keys
+//   at a time, as one contiguous stream per K and V. Loads carry the
+//   non-temporal hint: each row is read once.
 //   Keys go to workgroups in blocks of PH * U, dealt round-robin over the
 //   splits, so the launch sweeps the cache front to back as one window.
 //   Per iteration a slot holds U keys in registers, and the next iteration's
@@ -78,16 +79,19 @@ struct DecodeArgs {
 #define FLK_DECODE_NT 1  // K/V rows are read with the non-temporal hint (0: plain loads)
 #endif
 #ifndef FLK_DECODE_UNROLL
-#define FLK_DECODE_UNROLL 4
+#define FLK_DECODE_UNROLL 2
 #endif
-constexpr int kDecodeThreads = 256;
+#ifndef FLK_DECODE_THREADS
+#define FLK_DECODE_THREADS 512
+#endif
+constexpr int kDecodeThreads = FLK_DECODE_THREADS;
 constexpr int kMergeThreads = 256;
 constexpr int kMergeCols = 8;    // float4 columns per merge workgroup (32 channels)
 constexpr int kMergeBatch = 8;   // splits per thread per round of loads
 
 // Keys per slot per iteration: fewer when G is large, to bound registers.
 __host__ __device__ constexpr int decode_unroll(int G) {
-  return G <= 2 ? FLK_DECODE_UNROLL : (G <= 4 ? 4 : 2);
+  return G <= 4 ? FLK_DECODE_UNROLL : (FLK_DECODE_UNROLL > 1 ? FLK_DECODE_UNROLL / 2 : 1);
 }
 
 // Splits of a sequence with n_keys keys: ceil(blocks / bps), at most
