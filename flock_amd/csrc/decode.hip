@@ -73,7 +73,7 @@ struct DecodeArgs {
 #define FLK_DECODE_TARGET_WG 256
 #endif
 #ifndef FLK_DECODE_RAGGED_TARGET_WG
-#define FLK_DECODE_RAGGED_TARGET_WG 1024
+#define FLK_DECODE_RAGGED_TARGET_WG 4096
 #endif
 #ifndef FLK_DECODE_NT
 #define FLK_DECODE_NT 1  // K/V rows are read with the non-temporal hint (0: plain loads)
