@@ -30,8 +30,9 @@ N(1, 0.1)); caches are written on the device before timing starts.
 Timing: HIP events recorded on the stream the kernels are launched on bracket
 the K timed steps (after a synchronize). The roofline's average call duration
 is events around R back-to-back calls of the dominant entry point, divided by
-R; flk_decode_layer and flk_attn_prefill are each one call = the split kernel
-plus its merge kernel.
+R. One flk_decode_layer call is the split kernel plus its merge kernel; one
+flk_attn_prefill call is the prefill kernel, plus a merge kernel when the
+plan splits keys (chunk32k).
 """
 from __future__ import annotations
 
@@ -185,7 +186,7 @@ class Prefill2k(Workload):
     name = "prefill2k"
     unit = "TFLOP/s"
     bound = "mfma"
-    kernel = "flk_attn_prefill: prefill_kernel<128> + prefill_merge_kernel<128>"
+    kernel = "flk_attn_prefill: prefill_kernel<128> (paired q tiles, no merge launch)"
 
     def __init__(self, torch, ops, n=2048, pos0=0, layers=1):
         self.torch, self.ops = torch, ops
@@ -265,6 +266,7 @@ class Prefill2k(Workload):
 
 class Chunk32k(Prefill2k):
     name = "chunk32k"
+    kernel = "flk_attn_prefill: prefill_kernel<128> (key splits) + prefill_merge_kernel<128>"
 
     def __init__(self, torch, ops):
         super().__init__(torch, ops, n=64, pos0=32768, layers=28)

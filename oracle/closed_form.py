@@ -59,11 +59,11 @@ def attention(q, k, v, n_heads: int, n_kv_heads: int, head_dim: int, n_queries: 
     kvh = np.arange(H) // (H // Hkv)
     kh = k[:, kvh, :].transpose(1, 0, 2)            # [H][keys][d]
     vh = v[:, kvh, :].transpose(1, 0, 2)
-    s = np.einsum("qhd,hkd->hqk", q, kh) / np.sqrt(d)
+    s = np.matmul(q.transpose(1, 0, 2), kh.transpose(0, 2, 1)) / np.sqrt(d)  # [H][q][keys]
     mask = np.arange(n_keys)[None, :] > (pos0 + np.arange(n_queries))[:, None]
-    s = np.where(mask[None], -np.inf, s)
-    s = s - s.max(axis=2, keepdims=True)
-    p = np.exp(s)
-    p /= p.sum(axis=2, keepdims=True)
-    o = np.einsum("hqk,hkd->qhd", p, vh)
-    return o.ravel()
+    s[:, mask] = -np.inf
+    s -= s.max(axis=2, keepdims=True)
+    np.exp(s, out=s)
+    s /= s.sum(axis=2, keepdims=True)
+    o = np.matmul(s, vh)  # [H][q][d]
+    return o.transpose(1, 0, 2).ravel()
