@@ -353,8 +353,19 @@ class Copy(Workload):
 WORKLOADS = {c.name: c for c in (Decode32k, Prefill2k, Ragged, Chunk32k, Decode512, Copy)}
 
 
+def settle_clocks(torch, w, seconds=0.5):
+    """Untimed steps until `seconds` have passed, so the GPU is at its working
+    clock when the W warmup steps start (an idle GPU drops its clocks; the CPU
+    baselines and input generation leave it idle or differently loaded)."""
+    t0 = time.perf_counter()
+    while time.perf_counter() - t0 < seconds:
+        w.step()
+        torch.cuda.synchronize()
+
+
 def measure(torch, stream, w, steps, warmup, calls=None):
     """(ms per step, host wall ms per step, ms per dominant call)."""
+    settle_clocks(torch, w)
     for _ in range(warmup):
         w.step()
     torch.cuda.synchronize()
@@ -380,7 +391,8 @@ def measure(torch, stream, w, steps, warmup, calls=None):
     return ms, wall_ms, call_ms
 
 
-def run(torch, ops, stream, name, steps, warmup, cpu):
+def run(torch, ops, stream, name, steps, warmup):
+    """Measure one workload; returns its JSON fields and its CPU-baseline thunk."""
     w = WORKLOADS[name](torch, ops)
     torch.cuda.synchronize()
     log(f"[{name}] warmup {warmup}, timing {steps} steps")
@@ -391,12 +403,11 @@ def run(torch, ops, stream, name, steps, warmup, cpu):
     out = {"value": round(value, 3), "unit": w.unit, "ms_per_step": round(ms, 4),
            "config": w.config(),
            "roofline": w.roofline(call_ms, traffic_from_profiles(f"{name}_pmc.md"))}
-    if cpu:
-        log(f"[{name}] CPU baseline (oracle port, 1 thread)")
-        out["cpu_baseline"] = w.cpu_baseline()
-    del w
+    # Drop the device buffers; the CPU baseline needs only the sizes.
+    for k in [k for k, v in vars(w).items() if isinstance(v, (torch.Tensor, list, ops.Workspace))]:
+        delattr(w, k)
     torch.cuda.empty_cache()
-    return out
+    return out, w.cpu_baseline
 
 
 def main():
@@ -424,9 +435,8 @@ def main():
         sys.exit(1)
     stream = torch.cuda.Stream()
     ops.set_stream(stream)
-    cpu = not args.no_cpu_baseline
     with torch.cuda.stream(stream):
-        main_res = run(torch, ops, stream, args.workload, args.steps, args.warmup, cpu)
+        main_res, main_cpu = run(torch, ops, stream, args.workload, args.steps, args.warmup)
         out = {"metric": METRIC, "value": main_res["value"], "unit": main_res["unit"],
                "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                "ms_per_step": main_res["ms_per_step"], "higher_is_better": True,
@@ -438,12 +448,18 @@ def main():
             out["frac_of_hbm_peak"] = round(main_res["value"] / HBM_PEAK_GBS, 4)
         else:
             out["frac_of_fp32_mfma_peak"] = round(main_res["value"] / FP32_MFMA_PEAK_TFLOPS, 4)
+        pre_cpu = None
         if args.workload == "decode32k" and not args.no_secondary:
-            p = run(torch, ops, stream, "prefill2k", max(5, args.steps), args.warmup, cpu)
+            p, pre_cpu = run(torch, ops, stream, "prefill2k", max(5, args.steps), args.warmup)
             p["frac_of_fp32_mfma_peak"] = round(p["value"] / FP32_MFMA_PEAK_TFLOPS, 4)
             out["prefill"] = p
-        if "cpu_baseline" in main_res:
-            out["cpu_baseline"] = main_res["cpu_baseline"]
+    # CPU baselines last, with the GPU measurements done.
+    if not args.no_cpu_baseline:
+        log(f"[{args.workload}] CPU baseline (oracle port, 1 thread)")
+        out["cpu_baseline"] = main_cpu()
+        if pre_cpu is not None:
+            log("[prefill2k] CPU baseline (oracle port, 1 thread)")
+            out["prefill"]["cpu_baseline"] = pre_cpu()
     print(json.dumps(out), flush=True)
 
 

@@ -106,6 +106,16 @@ template <int D, int NPF = kBK * D / 4 / kPThreads>
 __device__ __forceinline__ void store_tile(const float4 (&pk)[NPF], const float4 (&pv)[NPF],
                                            float* k_lds, float* v_lds, uint32_t kt,
                                            uint32_t n_keys_total, int tid) {
+  if ((kt + 1) * kBK <= n_keys_total) {  // uniform: every row of the tile is live
+#pragma unroll
+    for (int i = 0; i < NPF; i++) {
+      const int f = tid + kPThreads * i;
+      const int rr = f / (D / 4), c4 = f % (D / 4);
+      *reinterpret_cast<float4*>(&k_lds[rr * (D + 4) + 4 * c4]) = pk[i];
+      *reinterpret_cast<float4*>(&v_lds[rr * D + 4 * c4]) = pv[i];
+    }
+    return;
+  }
 #pragma unroll
   for (int i = 0; i < NPF; i++) {
     const int f = tid + kPThreads * i;
