@@ -106,9 +106,6 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
   const int wave = threadIdx.x >> 6;
   const uint32_t tok = blockIdx.x;
   const uint32_t pos = pos0 + tok;
-  if (threadIdx.x < D / 2) s_cs[threadIdx.x] = rope_cos_sin(inv_freq[threadIdx.x], pos);
-  __syncthreads();
-
   const uint32_t per_tok = n_heads + 2 * n_kv_heads;
   const size_t kv_row = (size_t)n_kv_heads * D;
   // Vector idx -> (source, destination, gain): q heads, then k heads, then v.
@@ -129,14 +126,13 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
       dst = vcache + (size_t)pos * kv_row + (size_t)h * D;
     }
   };
-  const float gq0 = gq[lane], gq1 = D == 128 ? gq[lane + 64] : 0.f;
-  const float gk0 = gk[lane], gk1 = D == 128 ? gk[lane + 64] : 0.f;
   // Each wave takes vectors wave, wave + 4, ...; a batch of kBatch vectors is
-  // loaded before any is used, so their memory latency overlaps.
+  // loaded before any is used, so their memory latency overlaps. The first
+  // batch is requested before the cos/sin table is computed.
   constexpr int kWaves = kPrologueThreads / 64;
   constexpr int kBatch = 8;
-  for (uint32_t base = wave; base < per_tok; base += kWaves * kBatch) {
-    float e0[kBatch], e1[kBatch];
+  float e0[kBatch], e1[kBatch];
+  auto load_batch = [&](uint32_t base) {
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
       const uint32_t idx = min(base + kWaves * b, per_tok - 1);  // extras reload the last
@@ -147,6 +143,17 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
       e0[b] = src[lane];
       e1[b] = D == 128 ? src[lane + 64] : 0.f;
     }
+  };
+  // Loads retire in issue order: inv_freq first, so the table waits for it alone.
+  const float invf = inv_freq[min((int)threadIdx.x, D / 2 - 1)];
+  load_batch(wave);
+  const float gq0 = gq[lane], gq1 = D == 128 ? gq[lane + 64] : 0.f;
+  const float gk0 = gk[lane], gk1 = D == 128 ? gk[lane + 64] : 0.f;
+  if (threadIdx.x < D / 2) s_cs[threadIdx.x] = rope_cos_sin(invf, pos);
+  __syncthreads();
+
+  for (uint32_t base = wave; base < per_tok; base += kWaves * kBatch) {
+    if (base != (uint32_t)wave) load_batch(base);
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
       const uint32_t idx = base + kWaves * b;
