@@ -1,4 +1,4 @@
-"""ctypes binding of libflock_attn.so (declared in include/flock_attn.h).
+"""ctypes binding of libflock_attn.so (declared in include/flock_attn.h, flock_q8.h).
 
 This is the Python counterpart of the Deno.dlopen binding a TypeScript host
 would declare. The library is loaded from this package's directory only; if it
@@ -28,7 +28,7 @@ _i32 = ctypes.c_int32
 _u64 = ctypes.c_uint64
 _f32 = ctypes.c_float
 
-# name -> (restype, argtypes); the exact set of entry points in flock_attn.h.
+# name -> (restype, argtypes); the exact set of entry points in include/*.h.
 SIGNATURES: dict[str, tuple] = {
     "flk_last_error": (ctypes.c_char_p, []),
     "flk_version": (ctypes.c_char_p, []),
@@ -58,6 +58,9 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "flk_attn_decode_ragged": (
         _i32, [_p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32, _p, _u64]),
+    # include/flock_q8.h
+    "flk_q8_matvec": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32]),
+    "flk_q8_split": (_i32, [_p, _u32, _u32, _p, _p]),
 }
 
 

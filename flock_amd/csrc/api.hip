@@ -359,3 +359,43 @@ int32_t flk_attn_decode_ragged(const float* q, const float* kcache, const float*
 }
 
 }  // extern "C"
+
+// ------------------------------------------------------------- Q8_0 -------
+int32_t flk_q8_matvec(const int8_t* qs, const uint16_t* scales, const float* x, float* o,
+                      uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens) {
+  FLK_NONNULL(qs);
+  FLK_NONNULL(scales);
+  FLK_NONNULL(x);
+  FLK_NONNULL(o);
+  if (n_rows == 0 || n_cols == 0 || n_tokens == 0)
+    return fail(FLK_ERR_ARG, "q8_matvec n_rows=%u n_cols=%u n_tokens=%u", n_rows, n_cols,
+                n_tokens);
+  if (n_cols % 32 != 0) return fail(FLK_ERR_ARG, "q8_matvec n_cols %u is not a multiple of 32", n_cols);
+  if (n_tokens > 65535) return fail(FLK_ERR_UNSUPPORTED, "q8_matvec n_tokens %u > 65535", n_tokens);
+  FLK_ALIGNED(qs);
+  FLK_ALIGNED(x);
+  if (reinterpret_cast<uintptr_t>(scales) % 2 != 0)
+    return fail(FLK_ERR_ARG, "scales must be 2-byte aligned");
+  return hip_status(launch_q8_matvec(reinterpret_cast<const uint8_t*>(qs), scales, x, o, n_rows,
+                                     n_cols, n_tokens, g_stream),
+                    "flk_q8_matvec");
+}
+
+// splitQ8, kernels/lib.ts:141-156 (host memory only).
+int32_t flk_q8_split(const uint8_t* packed, uint32_t n_rows, uint32_t n_cols, int8_t* qs,
+                     uint16_t* scales) {
+  FLK_NONNULL(packed);
+  FLK_NONNULL(qs);
+  FLK_NONNULL(scales);
+  if (n_rows == 0 || n_cols == 0 || n_cols % 32 != 0)
+    return fail(FLK_ERR_ARG, "q8_split n_rows=%u n_cols=%u (n_cols a multiple of 32)", n_rows,
+                n_cols);
+  const uint32_t nb = n_cols / 32;
+  for (uint32_t r = 0; r < n_rows; r++)
+    for (uint32_t b = 0; b < nb; b++) {
+      const uint8_t* src = packed + ((uint64_t)r * nb + b) * 34;
+      scales[(uint64_t)r * nb + b] = (uint16_t)(src[0] | (src[1] << 8));
+      memcpy(qs + (uint64_t)r * n_cols + (uint64_t)b * 32, src + 2, 32);
+    }
+  return FLK_OK;
+}

@@ -5,6 +5,7 @@
 #include <stdint.h>
 
 #include "../../include/flock_attn.h"
+#include "../../include/flock_q8.h"
 #include "trig.hpp"
 
 namespace flk {
@@ -189,6 +190,10 @@ uint64_t prefill_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_d
 hipError_t launch_prefill(const float* q, const float* kcache, const float* vcache, float* o,
                           uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                           uint32_t n_queries, uint32_t pos0, void* ws, hipStream_t st);
+
+// ------------------------------------------------------------- Q8_0 matvec --
+hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const float* x, float* o,
+                            uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, hipStream_t st);
 
 // Workspace layout (split-K partials): [(m, l) pairs][pad to 256 B][acc rows].
 constexpr uint64_t kWsAlign = 256;

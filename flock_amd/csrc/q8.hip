@@ -1,0 +1,224 @@
+// Q8_0 dequantizing matvec: the projections on either side of attention.
+//
+// Weights arrive in the reference's split layout (kernels/lib.ts:141-156):
+// `qs` holds each row's int8 quants contiguously, `scales` one f16 per 32
+// quants. out[t][r] = sum_c W[r][c] * x[t][c] with W[r][c] = scale * q.
+//
+// Summation order is the reference's cooperative one (q8_coop.wgsl:96-140,
+// cpuMatmulQ8F32 with coop(64), kernels/lib.ts:196-278), so results are
+// identical to it, not merely close:
+//   logical lane l (0..63) of a row owns blocks l, l + 64, ... in order;
+//   per block and word pair g: d0 = dot4(q[8g..8g+3], x), d1 = dot4(q[8g+4..
+//   8g+7], x) with dot4 = one rounded product then three FMAs, and
+//   part = fma(scale, d0 + d1, part);
+//   the 64 partials are summed by the pairwise tree (stride 32, 16, ..., 1),
+//   done here as an xor butterfly (f32 addition is commutative).
+//
+// Layout on the GPU: a row needs P = min(64, pow2 >= blocks per row) logical
+// lanes (lanes past the row's block count hold 0 and the tree adds them as
+// exact zeros), so a wave covers 64 / P rows at once (2 for 1024 columns).
+// Lane l's x slice (blocks l, l + 64, ...) is the same for every row: it is
+// loaded into registers once per wave and the row loop streams only the
+// weights, several row groups in flight. Tokens of a batch ride on grid y
+// (q8_coop.wgsl:28-35); each re-reads the weights, from L2 when they fit.
+#include "common.hpp"
+
+namespace flk {
+
+constexpr int kQ8Lanes = 64;      // the reference's LANES (q8_coop.wgsl:58)
+constexpr int kQ8Threads = 256;   // 4 waves
+// Row groups whose loads are in flight together (fewer when x takes more registers).
+template <int NB>
+constexpr int q8_unroll() { return NB == 1 ? 4 : (NB == 2 ? 2 : 1); }
+constexpr int kQ8MaxRegBlocks = 4;  // x blocks per lane kept in registers (8192 columns)
+
+struct Q8Args {
+  const uint8_t* qs;
+  const uint16_t* scales;
+  const float* x;
+  float* o;
+  uint32_t n_rows, n_cols, n_tokens;
+};
+
+// halfToF32 (kernels/lib.ts:28-33): exact for every finite f16 (subnormals
+// included); exponent 31 (inf, nan) becomes +-3.4028235e38, the largest f32.
+__device__ __forceinline__ float q8_scale(uint16_t h) {
+  if ((h & 0x7c00u) == 0x7c00u) return (h & 0x8000u) ? -3.40282347e38f : 3.40282347e38f;
+  return (float)__builtin_bit_cast(_Float16, h);
+}
+
+// int8 quant k (0..3) of a little-endian word as f32.
+__device__ __forceinline__ float q8_quant(uint32_t w, int k) {
+  return (float)((int32_t)(w << (24 - 8 * k)) >> 24);
+}
+
+// dot(vec4, vec4) as the reference's GPU evaluates it: the first product
+// rounded, the other three fused.
+__device__ __forceinline__ float q8_dot4(uint32_t w, const float* x) {
+  float s = q8_quant(w, 0) * x[0];
+  s = __builtin_fmaf(q8_quant(w, 1), x[1], s);
+  s = __builtin_fmaf(q8_quant(w, 2), x[2], s);
+  s = __builtin_fmaf(q8_quant(w, 3), x[3], s);
+  return s;
+}
+
+// One 32-quant block folded into a lane's partial (q8_coop.wgsl:105-112).
+__device__ __forceinline__ float q8_block(float part, float scale, uint4 w0, uint4 w1,
+                                          const float* x) {
+  const uint32_t w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    const float d0 = q8_dot4(w[2 * g], x + 8 * g);
+    const float d1 = q8_dot4(w[2 * g + 1], x + 8 * g + 4);
+    part = __builtin_fmaf(scale, d0 + d1, part);
+  }
+  return part;
+}
+
+// P logical lanes per row, NB x blocks per lane in registers (NB * 64 >= the
+// row's block count). Grid: (workgroups over row groups, tokens).
+template <int P, int NB>
+__global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
+  constexpr int R = kWave / P;  // rows per wave per step
+  constexpr int kQ8Unroll = q8_unroll<NB>();
+  const int lane = threadIdx.x & 63;
+  const int ll = lane % P;      // logical lane
+  const int sub = lane / P;     // which row of the group
+  const uint32_t tok = blockIdx.y;
+  const uint32_t nb = a.n_cols / 32;
+  const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
+  const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
+
+  // x blocks ll, ll + 64, ... of this token (zeros past the row's end).
+  float xr[NB][32];
+  bool live[NB];
+#pragma unroll
+  for (int j = 0; j < NB; j++) {
+    const uint32_t b = ll + kQ8Lanes * j;
+    live[j] = b < nb;
+    const float4* xs = reinterpret_cast<const float4*>(a.x + (size_t)tok * a.n_cols +
+                                                       32 * (size_t)min(b, nb - 1));
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      const float4 v = xs[i];
+      xr[j][4 * i + 0] = v.x;
+      xr[j][4 * i + 1] = v.y;
+      xr[j][4 * i + 2] = v.z;
+      xr[j][4 * i + 3] = v.w;
+    }
+  }
+
+  const uint32_t n_groups = (a.n_rows + R - 1) / R;
+  for (uint32_t g0 = wave; g0 < n_groups; g0 += waves * kQ8Unroll) {
+    // Loads of kQ8Unroll row groups first (rows past the end re-read the last
+    // row, so every load is unconditional), then the arithmetic.
+    uint4 w0[kQ8Unroll][NB], w1[kQ8Unroll][NB];
+    uint16_t hs[kQ8Unroll][NB];
+#pragma unroll
+    for (int u = 0; u < kQ8Unroll; u++) {
+      const uint32_t row = min((g0 + waves * u) * R + sub, a.n_rows - 1);
+#pragma unroll
+      for (int j = 0; j < NB; j++) {
+        const uint32_t b = min((uint32_t)(ll + kQ8Lanes * j), nb - 1);
+        const uint4* src = reinterpret_cast<const uint4*>(a.qs + (size_t)row * a.n_cols + 32 * (size_t)b);
+        w0[u][j] = src[0];
+        w1[u][j] = src[1];
+        hs[u][j] = a.scales[(size_t)row * nb + b];
+      }
+    }
+#pragma unroll
+    for (int u = 0; u < kQ8Unroll; u++) {
+      float part = 0.f;
+#pragma unroll
+      for (int j = 0; j < NB; j++)
+        if (live[j]) part = q8_block(part, q8_scale(hs[u][j]), w0[u][j], w1[u][j], xr[j]);
+      // The reference's tree over 64 partials; strides >= P add exact zeros.
+#pragma unroll
+      for (int m = P / 2; m >= 1; m >>= 1) part += shfl_xor(part, m);
+      const uint32_t row = (g0 + waves * u) * R + sub;
+      if (ll == 0 && g0 + waves * u < n_groups && row < a.n_rows)
+        a.o[(size_t)tok * a.n_rows + row] = part;
+    }
+  }
+}
+
+// Columns past kQ8MaxRegBlocks * 64 blocks: the same arithmetic with x read
+// from memory per block (L1/L2-resident), one row per wave.
+__global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
+  const int lane = threadIdx.x & 63;
+  const uint32_t tok = blockIdx.y;
+  const uint32_t nb = a.n_cols / 32;
+  const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
+  const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
+  const float* xt = a.x + (size_t)tok * a.n_cols;
+  for (uint32_t row = wave; row < a.n_rows; row += waves) {
+    float part = 0.f;
+    for (uint32_t b = lane; b < nb; b += kQ8Lanes) {
+      const uint4* src = reinterpret_cast<const uint4*>(a.qs + (size_t)row * a.n_cols + 32 * (size_t)b);
+      float xb[32];
+      const float4* xs = reinterpret_cast<const float4*>(xt + 32 * (size_t)b);
+#pragma unroll
+      for (int i = 0; i < 8; i++) {
+        const float4 v = xs[i];
+        xb[4 * i + 0] = v.x;
+        xb[4 * i + 1] = v.y;
+        xb[4 * i + 2] = v.z;
+        xb[4 * i + 3] = v.w;
+      }
+      part = q8_block(part, q8_scale(a.scales[(size_t)row * nb + b]), src[0], src[1], xb);
+    }
+#pragma unroll
+    for (int m = 32; m >= 1; m >>= 1) part += shfl_xor(part, m);
+    if (lane == 0) a.o[(size_t)tok * a.n_rows + row] = part;
+  }
+}
+
+// Workgroups: enough waves to keep ~8 per SIMD busy, never more than there
+// are row groups.
+static uint32_t q8_grid_x(uint32_t n_groups, int unroll) {
+  const uint32_t per_wg = (kQ8Threads / kWave) * unroll;
+  const uint32_t need = (n_groups + per_wg - 1) / per_wg;
+  const uint32_t cap = 256 * 8;
+  return need < cap ? (need > 0 ? need : 1) : cap;
+}
+
+template <int P, int NB>
+static void launch_q8(const Q8Args& a, hipStream_t st) {
+  const uint32_t groups = (a.n_rows + (kWave / P) - 1) / (kWave / P);
+  hipLaunchKernelGGL((q8_matvec_kernel<P, NB>), dim3(q8_grid_x(groups, q8_unroll<NB>()), a.n_tokens),
+                     dim3(kQ8Threads), 0, st, a);
+}
+
+hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const float* x, float* o,
+                            uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
+                            hipStream_t st) {
+  Q8Args a{qs, scales, x, o, n_rows, n_cols, n_tokens};
+  const uint32_t nb = n_cols / 32;
+  if (nb > (uint32_t)kQ8Lanes * kQ8MaxRegBlocks) {
+    const uint32_t wg = (n_rows + 3) / 4 < 2048u ? (n_rows + 3) / 4 : 2048u;
+    hipLaunchKernelGGL(q8_matvec_wide_kernel, dim3(wg, n_tokens), dim3(kQ8Threads), 0, st, a);
+  } else if (nb > 192) {
+    launch_q8<64, 4>(a, st);
+  } else if (nb > 128) {
+    launch_q8<64, 3>(a, st);
+  } else if (nb > 64) {
+    launch_q8<64, 2>(a, st);
+  } else if (nb > 32) {
+    launch_q8<64, 1>(a, st);
+  } else if (nb > 16) {
+    launch_q8<32, 1>(a, st);
+  } else if (nb > 8) {
+    launch_q8<16, 1>(a, st);
+  } else if (nb > 4) {
+    launch_q8<8, 1>(a, st);
+  } else if (nb > 2) {
+    launch_q8<4, 1>(a, st);
+  } else if (nb > 1) {
+    launch_q8<2, 1>(a, st);
+  } else {
+    launch_q8<1, 1>(a, st);
+  }
+  return hipGetLastError();
+}
+
+}  // namespace flk

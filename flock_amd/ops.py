@@ -196,3 +196,44 @@ def attn_decode_ragged(q, kcache, vcache, seq_row_off, n_keys, o, n_seqs: int, m
     check(lib().flk_attn_decode_ragged(ptr(q), ptr(kcache), ptr(vcache), ptr(seq_row_off),
                                        ptr(n_keys), ptr(o), n_seqs, max_n_keys, n_heads,
                                        n_kv_heads, head_dim, w, nb), "flk_attn_decode_ragged")
+
+
+# ------------------------------------------------------------ Q8_0 projections
+def q8_split(packed, n_rows: int, n_cols: int):
+    """splitQ8 (kernels/lib.ts:141-156) on the host: GGUF Q8_0 bytes -> (qs int8, scales f16 bits)."""
+    packed = np.ascontiguousarray(packed, dtype=np.uint8)
+    if n_cols % 32 or packed.size != n_rows * n_cols // 32 * 34:
+        raise ValueError(f"{packed.size} bytes is not {n_rows} x {n_cols} Q8_0")
+    qs = np.empty(n_rows * n_cols, np.int8)
+    sc = np.empty(n_rows * n_cols // 32, np.uint16)
+    check(lib().flk_q8_split(packed.ctypes.data, n_rows, n_cols, qs.ctypes.data, sc.ctypes.data),
+          "flk_q8_split")
+    return qs, sc
+
+
+class Q8Matrix:
+    """One Q8_0 weight matrix resident on the device (the reference's
+    `wq[name]` = {qs, sc, rows, cols}, kernels/layer.ts:430-448)."""
+
+    def __init__(self, qs, scales, n_rows: int, n_cols: int):
+        self.rows, self.cols = n_rows, n_cols
+        self.qs = DeviceBuffer.from_array(np.ascontiguousarray(qs, np.int8))
+        self.scales = DeviceBuffer.from_array(np.ascontiguousarray(scales, np.uint16))
+
+    @classmethod
+    def from_packed(cls, packed, n_rows: int, n_cols: int) -> "Q8Matrix":
+        qs, sc = q8_split(packed, n_rows, n_cols)
+        return cls(qs, sc, n_rows, n_cols)
+
+
+def q8_matvec(w, x, o, n_tokens: int = 1, qs=None, scales=None, n_rows: int | None = None,
+              n_cols: int | None = None) -> None:
+    """Layer.matvec (kernels/layer.ts:495-510): o[t] = W x[t] for t < n_tokens.
+
+    ``w`` is a Q8Matrix, or None with ``qs``/``scales``/``n_rows``/``n_cols``
+    given as device buffers and sizes.
+    """
+    if w is not None:
+        qs, scales, n_rows, n_cols = w.qs, w.scales, w.rows, w.cols
+    check(lib().flk_q8_matvec(ptr(qs), ptr(scales), ptr(x), ptr(o), n_rows, n_cols, n_tokens),
+          "flk_q8_matvec")

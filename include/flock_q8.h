@@ -1,0 +1,45 @@
+/*
+ * flock_q8.h -- C ABI of the Q8_0 projections in libflock_attn.so.
+ *
+ * The projections immediately before and after the attention path: q/k/v from
+ * the hidden state and o back to it (kernels/layer.ts:495-510, Layer.matvec,
+ * dispatching kernels/q8_coop.wgsl). Same conventions as flock_attn.h: device
+ * pointers for tensors, FLK_OK or a negative FLK_ERR_* code with
+ * flk_last_error(), work queued on the stream set by flk_set_stream().
+ *
+ * Weights use the reference's upload layout (kernels/lib.ts:141-156, splitQ8):
+ *   qs     [n_rows][n_cols] int8 quants, row-major;
+ *   scales [n_rows][n_cols / 32] f16 bit patterns, one per 32-quant block.
+ * flk_q8_split builds both from GGUF's 34-byte Q8_0 blocks on the host.
+ */
+#ifndef FLOCK_Q8_H
+#define FLOCK_Q8_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* o[t][r] = sum_c scale(r, c / 32) * qs[r][c] * x[t][c] for t < n_tokens.
+ * Replaces Layer.matvec (kernels/layer.ts:495-510) / q8_coop.wgsl:74-140 with
+ * Dims {n_rows, n_cols, n_tokens}: x is [n_tokens][n_cols], o is
+ * [n_tokens][n_rows]. n_cols must be a multiple of 32; n_tokens <= 65535.
+ * qs and x must be 16-byte aligned. Results are bit-identical to
+ * cpuMatmulQ8F32(..., coop(64)) (kernels/lib.ts:251-278) with each
+ * multiply-add as one rounding; scales with exponent 31 read as +-FLT_MAX
+ * (halfToF32, kernels/lib.ts:28-33). */
+int32_t flk_q8_matvec(const int8_t* qs, const uint16_t* scales, const float* x, float* o,
+                      uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens);
+
+/* splitQ8 (kernels/lib.ts:141-156) on the host: packed is n_rows * n_cols / 32
+ * blocks of 34 bytes (f16 scale, little-endian, then 32 int8); writes qs
+ * [n_rows * n_cols] and scales [n_rows * n_cols / 32]. HOST pointers. */
+int32_t flk_q8_split(const uint8_t* packed, uint32_t n_rows, uint32_t n_cols, int8_t* qs,
+                     uint16_t* scales);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* FLOCK_Q8_H */

@@ -8,6 +8,8 @@ Two independent formulations live here:
 * ``flock_oracle.c`` (wrapped below): the reference's strict-f32 CPU oracle
   restated rounding point for rounding point (kernels/ops_ref.ts,
   kernels/head_ref.ts, kernels/layer_ref.ts, kernels/lib.ts:169-171).
+* ``flock_oracle_q8.c``: the Q8_0 projection references (kernels/lib.ts:28-53,
+  141-156, 196-278; web/js/wire.mjs:33-53).
 * ``closed_form``: textbook float64 formulas (softmax(q k^T / sqrt d) v with
   the GQA map and causal bound, RMSNorm, rotation) used to pin the
   restatement. They share no code with it.
@@ -32,6 +34,7 @@ QWEN3_EPS = 9.999999974752427e-7
 QWEN3_ROPE_BASE = 1e6
 
 _f32p = ctypes.POINTER(ctypes.c_float)
+_u8p = ctypes.POINTER(ctypes.c_uint8)
 
 
 def build() -> str:
@@ -66,6 +69,11 @@ def lib() -> ctypes.CDLL:
                 [_f32p] * 6 + [d, i] + [_f32p] * 4 + [i, i, i, i, i],
             ),
             "flko_set_threads": (i, [i]),
+            "flko_f32_to_f16": (ctypes.c_uint16, [ctypes.c_float]),
+            "flko_half_to_f32": (d, [ctypes.c_uint16]),
+            "flko_quant_row_q8": (None, [_f32p, i64, _u8p]),
+            "flko_split_q8": (None, [_u8p, i, i, _u8p, _u8p]),
+            "flko_q8_matvec": (None, [_u8p, _f32p, i, i, i, i, _f32p]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -200,3 +208,74 @@ def layer_attn_prefill(q_raw, k_raw, v_raw, gq, gk, inv_freq, kcache: np.ndarray
                                   _p(kcache), _p(vcache), _p(qn), _p(o), n, pos0, n_heads,
                                   n_kv_heads, head_dim)
     return qn, o
+
+
+# ---------------------------------------------------------------- Q8_0 ------
+Q8_BLOCK, Q8_BYTES = 32, 34
+
+
+def _u8(a) -> np.ndarray:
+    return np.ascontiguousarray(a, dtype=np.uint8)
+
+
+def _pu8(a: np.ndarray):
+    return a.ctypes.data_as(_u8p)
+
+
+def f32_to_f16(v) -> int:
+    """f32to16, web/js/wire.mjs:33-53 (f16 bits of an f32, round to nearest even)."""
+    return int(lib().flko_f32_to_f16(float(np.float32(v))))
+
+
+def f32_to_f16_array(a) -> np.ndarray:
+    a = _f32(a).ravel()
+    f = lib().flko_f32_to_f16
+    return np.array([f(float(v)) for v in a], dtype=np.uint16)
+
+
+def half_to_f32(h: int) -> float:
+    """halfToF32, kernels/lib.ts:28-33 (exponent 31 clamps to +-3.4028235e38)."""
+    return float(lib().flko_half_to_f32(int(h) & 0xFFFF))
+
+
+def quant_matrix_q8(w, rows: int, cols: int) -> np.ndarray:
+    """quantMatrixQ8 / quantRowQ8, kernels/lib.ts:38-53, 102-109: 34-byte blocks.
+
+    Rows are concatenations of independent 32-value blocks, so the whole
+    matrix goes through quantRowQ8's block loop in one call.
+    """
+    w = _f32(w).ravel()
+    assert w.size == rows * cols and cols % Q8_BLOCK == 0
+    out = np.empty(rows * cols // Q8_BLOCK * Q8_BYTES, np.uint8)
+    lib().flko_quant_row_q8(_p(w), rows * cols, _pu8(out))
+    return out
+
+
+def split_q8(packed, rows: int, cols: int):
+    """splitQ8, kernels/lib.ts:141-156: (qs int8 [rows*cols], scales f16 bits [rows*cols/32])."""
+    packed = _u8(packed)
+    assert packed.size == rows * cols // Q8_BLOCK * Q8_BYTES
+    qs = np.empty(rows * cols, np.uint8)
+    sc = np.empty(rows * cols // Q8_BLOCK * 2, np.uint8)
+    lib().flko_split_q8(_pu8(packed), rows, cols, _pu8(qs), _pu8(sc))
+    return qs.view(np.int8), sc.view(np.uint16)
+
+
+def q8_matvec(packed, x, rows: int, cols: int, lanes: int = 64, fused: bool = False) -> np.ndarray:
+    """cpuMatmulQ8F32, kernels/lib.ts:196-278: W (34-byte Q8_0 blocks) times x.
+
+    ``lanes=0`` is SERIAL (q8_matmul.wgsl), ``lanes=64`` is coop(64)
+    (q8_coop.wgsl). ``fused`` swaps the reference's fma32 (two roundings) for
+    a one-rounding fmaf. ``x`` may hold several tokens ([n_tokens][cols]).
+    """
+    packed, x = _u8(packed), _f32(x)
+    assert packed.size == rows * cols // Q8_BLOCK * Q8_BYTES and x.size % cols == 0
+    assert lanes == 0 or (lanes & (lanes - 1) == 0 and lanes <= 1024)
+    nt = x.size // cols
+    out = np.empty(nt * rows, np.float32)
+    for t in range(nt):
+        xt = np.ascontiguousarray(x[t * cols:(t + 1) * cols])
+        ot = np.empty(rows, np.float32)
+        lib().flko_q8_matvec(_pu8(packed), _p(xt), rows, cols, lanes, int(bool(fused)), _p(ot))
+        out[t * rows:(t + 1) * rows] = ot
+    return out

@@ -1,7 +1,7 @@
 """The drop-in boundary, checked without a GPU.
 
-* libflock_attn.so loads and exports every function include/flock_attn.h
-  declares, and the ctypes table in flock_amd/_lib.py binds exactly that set.
+* libflock_attn.so loads and exports every function include/*.h declares,
+  and the ctypes table in flock_amd/_lib.py binds exactly that set.
 * Host-side guards run before any launch and return the documented status
   (the reference throws from Layer before encoding: layer.ts:575, 689-698;
   lib.ts:504-506). Garbage non-null pointers are safe here because a rejected
@@ -18,14 +18,21 @@ import pytest
 from flock_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
-HEADER = os.path.join(ROOT, "include", "flock_attn.h")
+HEADERS = [os.path.join(ROOT, "include", h) for h in ("flock_attn.h", "flock_q8.h")]
 FAKE = 0x1000  # never dereferenced: every call below fails validation first
 
 
 def declared_functions() -> set[str]:
-    text = open(HEADER).read()
-    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
-    return set(re.findall(r"\b(flk_\w+)\s*\(", text))
+    names = set()
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        names |= set(re.findall(r"\b(flk_\w+)\s*\(", text))
+    return names
+
+
+def test_every_header_is_listed():
+    assert sorted(os.path.basename(h) for h in HEADERS) == sorted(
+        f for f in os.listdir(os.path.join(ROOT, "include")) if f.endswith(".h"))
 
 
 def test_header_and_binding_agree():
@@ -121,3 +128,32 @@ def test_ragged_workspace_bound():
         for maxn in (1, 100, 1024, 5000, 16385):
             for s in range(1, seqs + 1, max(1, seqs // 7)):
                 assert 0 <= L.flk_call_workspace_bytes(2, 16, 8, 128, maxn, 0, s) <= ws
+
+
+def test_q8_matvec_guards():
+    L = _lib.lib()
+    rc, msg = code_and_msg(L.flk_q8_matvec(FAKE, FAKE, FAKE, FAKE, 16, 48, 1))
+    assert rc == _lib.FLK_ERR_ARG and "multiple of 32" in msg
+    rc, msg = code_and_msg(L.flk_q8_matvec(FAKE, FAKE, FAKE, FAKE, 0, 64, 1))
+    assert rc == _lib.FLK_ERR_ARG
+    rc, msg = code_and_msg(L.flk_q8_matvec(FAKE, FAKE, FAKE, FAKE, 16, 64, 70000))
+    assert rc == _lib.FLK_ERR_UNSUPPORTED
+    rc, msg = code_and_msg(L.flk_q8_matvec(FAKE + 4, FAKE, FAKE, FAKE, 16, 64, 1))
+    assert rc == _lib.FLK_ERR_ARG and "aligned" in msg
+    rc, msg = code_and_msg(L.flk_q8_matvec(None, FAKE, FAKE, FAKE, 16, 64, 1))
+    assert rc == _lib.FLK_ERR_ARG and "null" in msg
+
+
+def test_q8_split_matches_oracle():
+    # Host-side repack (no GPU): the library's splitQ8 against the oracle's.
+    import numpy as np
+    import oracle
+    rng = np.random.default_rng(3)
+    rows, cols = 5, 96
+    packed = oracle.quant_matrix_q8(rng.normal(0, 0.05, rows * cols), rows, cols)
+    qs = np.empty(rows * cols, np.int8)
+    sc = np.empty(rows * cols // 32, np.uint16)
+    assert _lib.lib().flk_q8_split(packed.ctypes.data, rows, cols, qs.ctypes.data,
+                                   sc.ctypes.data) == 0
+    want_qs, want_sc = oracle.split_q8(packed, rows, cols)
+    assert np.array_equal(qs, want_qs) and np.array_equal(sc, want_sc)

@@ -1,0 +1,114 @@
+"""flk_q8_matvec on the GPU against the Q8_0 oracle, bit for bit.
+
+The kernel follows q8_coop.wgsl's summation order (coop(64) in
+cpuMatmulQ8F32, kernels/lib.ts:196-278) with one-rounding FMAs, so every
+output must equal the oracle's (fused=True) exactly. Shapes cover the Qwen3
+projections (q 2048x1024, k/v 1024x1024, o 1024x2048, gate/up 3072x1024,
+down 1024x3072, LM head 151936x1024), every lanes-per-row layout (1..64 and
+2-4 blocks per lane), the wide fallback (> 8192 columns), batched tokens and
+the f16 scale edge cases (subnormal, exponent 31).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+
+pytestmark = pytest.mark.gpu
+
+from flock_amd import ops  # noqa: E402
+
+
+def run_gpu(packed, x, rows, cols, n_tokens=1):
+    w = ops.Q8Matrix.from_packed(packed, rows, cols)
+    xb = ops.DeviceBuffer.from_array(np.ascontiguousarray(x, np.float32))
+    ob = ops.DeviceBuffer(n_tokens * rows * 4)
+    ops.q8_matvec(w, xb, ob, n_tokens)
+    ops.sync()
+    return ob.download(n_tokens * rows)
+
+
+def problem(rng, rows, cols, n_tokens=1, wscale=0.05):
+    packed = oracle.quant_matrix_q8((rng.standard_normal(rows * cols) * wscale).astype(np.float32),
+                                    rows, cols)
+    x = rng.standard_normal(n_tokens * cols).astype(np.float32)
+    return packed, x
+
+
+@pytest.mark.parametrize("rows,cols", [
+    (2048, 1024), (1024, 1024), (1024, 2048), (3072, 1024), (1024, 3072),  # Qwen3 projections
+    (4096, 1024),                                   # q, k, v stacked
+    (64, 32), (33, 64), (17, 96), (9, 160), (5, 288), (130, 512),  # 1..16 lanes per row
+    (70, 4096), (40, 6144), (24, 8192),             # 2, 3, 4 blocks per lane
+    (13, 8224),                                     # wide path (257 blocks)
+    (1, 1024), (3, 1024),                           # fewer rows than a wave covers
+])
+def test_matches_oracle_exactly(rng, rows, cols):
+    packed, x = problem(rng, rows, cols)
+    got = run_gpu(packed, x, rows, cols)
+    want = oracle.q8_matvec(packed, x, rows, cols, 64, fused=True)
+    assert np.array_equal(got, want), np.flatnonzero(got != want)[:8]
+    # The reference's own CPU model (two roundings per fma32) agrees too.
+    assert np.array_equal(got, oracle.q8_matvec(packed, x, rows, cols, 64, fused=False))
+
+
+@pytest.mark.parametrize("n_tokens", [2, 3, 7])
+def test_batched_tokens(rng, n_tokens):
+    rows, cols = 1024, 1024
+    packed, x = problem(rng, rows, cols, n_tokens)
+    got = run_gpu(packed, x, rows, cols, n_tokens)
+    want = oracle.q8_matvec(packed, x, rows, cols, 64, fused=True)
+    assert np.array_equal(got, want)
+
+
+def random_packed(rng, rows, cols):
+    """Q8_0 bytes with random int8 quants and f16 scales around 4e-4 (what
+    quantRowQ8 gives for N(0, 0.05) weights), built without the quantizer."""
+    blocks = np.empty((rows * cols // 32, 34), np.uint8)
+    sc = (np.abs(rng.standard_normal(blocks.shape[0])) * 4e-4 + 1e-5).astype(np.float16)
+    blocks[:, :2] = sc.view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:] = rng.integers(0, 256, (blocks.shape[0], 32), dtype=np.uint8)
+    return blocks.ravel()
+
+
+def test_lm_head_shape(rng):
+    # Qwen3-0.6B's tied LM head: 151936 x 1024 (165 MB of Q8_0).
+    rows, cols = 151936, 1024
+    packed = random_packed(rng, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    got = run_gpu(packed, x, rows, cols)
+    want = oracle.q8_matvec(packed, x, rows, cols, 64, fused=True)
+    assert np.array_equal(got, want)
+    assert oracle.argmax(got) == oracle.argmax(want)
+
+
+def test_scale_edge_cases(rng):
+    # Subnormal, tiny normal, largest finite and exponent-31 scales (inf and
+    # nan patterns read as +-FLT_MAX); x small so products stay finite.
+    rows, cols = 8, 64
+    scales = [0x0001, 0x03FF, 0x0400, 0x7BFF, 0x7C00, 0xFC00, 0x7E00, 0x3C00]
+    q = rng.integers(-128, 128, (rows, cols))
+    parts = []
+    for r in range(rows):
+        for b in range(cols // 32):
+            h = scales[r]
+            parts.append(bytes([h & 0xFF, h >> 8]) +
+                         bytes((q[r, 32 * b:32 * b + 32] & 0xFF).astype(np.uint8)))
+    packed = np.frombuffer(b"".join(parts), np.uint8)
+    x = (rng.standard_normal(cols) * 1e-3).astype(np.float32)
+    got = run_gpu(packed, x, rows, cols)
+    want = oracle.q8_matvec(packed, x, rows, cols, 64, fused=True)
+    assert np.array_equal(got, want)
+
+
+def test_integer_problem_is_exact(rng):
+    # Integer quants, unit scales, integer x: the exact product, whatever the order.
+    rows, cols = 512, 2048
+    q = rng.integers(-128, 128, (rows, cols))
+    x = rng.integers(-8, 9, cols).astype(np.float32)
+    packed = np.frombuffer(b"".join(
+        bytes([0x00, 0x3C]) + bytes((q[r, 32 * b:32 * b + 32] & 0xFF).astype(np.uint8))
+        for r in range(rows) for b in range(cols // 32)), np.uint8)
+    got = run_gpu(packed, x, rows, cols)
+    assert np.array_equal(got, (q @ x.astype(np.int64)).astype(np.float32))

@@ -1,0 +1,185 @@
+"""Pins the Q8_0 oracle (oracle/flock_oracle_q8.c) before it judges the GPU.
+
+Each check is independent of the restated code: numpy's IEEE float16
+conversions, exact integer arithmetic, hand-derived expected values of the
+reference's algorithm (kernels/lib.ts:28-53, 141-156, 196-318;
+web/js/wire.mjs:33-53), and an f64 error bound.
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+import oracle
+
+F32_MAX = float(np.finfo(np.float32).max)
+
+
+def block(scale_bits: int, q) -> bytes:
+    q = np.asarray(q, np.int64)
+    assert q.size == 32
+    return bytes([scale_bits & 0xFF, scale_bits >> 8]) + bytes((q & 0xFF).astype(np.uint8))
+
+
+# ---------------------------------------------------------------- f32 -> f16
+def test_f32_to_f16_matches_ieee_round_to_nearest_even():
+    rng = np.random.default_rng(0)
+    vals = np.concatenate([
+        rng.standard_normal(4000).astype(np.float32),
+        (rng.standard_normal(2000) * 1e-5).astype(np.float32),        # f16 subnormals
+        (rng.standard_normal(2000) * 1e-8).astype(np.float32),        # below / near 2^-24
+        (rng.standard_normal(2000) * 3e4).astype(np.float32),         # near the top
+        np.array([65504, 65519.99, 65520, 1e6, -1e6, 0.0, -0.0, 2.0 ** -24, 2.0 ** -25,
+                  3 * 2.0 ** -26, 2.0 ** -14, 1 + 2.0 ** -11, 1 + 3 * 2.0 ** -11, np.inf,
+                  -np.inf], np.float32),
+    ])
+    with np.errstate(over="ignore"):
+        want = vals.astype(np.float16).view(np.uint16)
+    got = oracle.f32_to_f16_array(vals)
+    assert np.array_equal(got, want)
+
+
+def test_f32_to_f16_ties_and_nan():
+    # 1 + 2^-11 lies halfway between 1 and 1 + 2^-10: even wins (1.0 = 0x3C00);
+    # 1 + 3 * 2^-11 lies halfway between 1 + 2^-10 and 1 + 2^-9: 0x3C02.
+    assert oracle.f32_to_f16(1 + 2.0 ** -11) == 0x3C00
+    assert oracle.f32_to_f16(1 + 3 * 2.0 ** -11) == 0x3C02
+    assert oracle.f32_to_f16(float("nan")) & 0x7FFF == 0x7E00
+    assert oracle.f32_to_f16(-65520.0) == 0xFC00  # rounds past the largest finite: -inf
+
+
+# ---------------------------------------------------------------- f16 -> f32
+def test_half_to_f32_all_patterns():
+    h = np.arange(65536, dtype=np.uint32).astype(np.uint16)
+    want = h.view(np.float16).astype(np.float64)
+    exp31 = (h & 0x7C00) == 0x7C00
+    want[exp31] = np.where(h[exp31] & 0x8000, -3.4028235e38, 3.4028235e38)
+    got = np.array([oracle.half_to_f32(int(v)) for v in h])
+    assert np.array_equal(got[~exp31], want[~exp31])
+    assert np.array_equal(got[exp31], want[exp31])
+    # Rounded to f32 (as cpuMatmulQ8F32 does with fr) the clamp is FLT_MAX.
+    assert np.float32(oracle.half_to_f32(0x7C00)) == np.float32(F32_MAX)
+
+
+# ---------------------------------------------------------------- quantizer
+def test_quant_row_invariants():
+    rng = np.random.default_rng(1)
+    rows, cols = 8, 256
+    w = (rng.standard_normal(rows * cols) * 0.05).astype(np.float32)
+    w[:32] = 0.0  # an all-zero block
+    packed = oracle.quant_matrix_q8(w, rows, cols).reshape(-1, 34)
+    vals = w.reshape(-1, 32).astype(np.float64)
+    for b in range(packed.shape[0]):
+        h = int(packed[b, 0]) | (int(packed[b, 1]) << 8)
+        q = packed[b, 2:].view(np.int8).astype(np.float64)
+        amax = np.max(np.abs(vals[b]))
+        d = amax / 127
+        assert h == oracle.f32_to_f16(np.float32(d))
+        if amax == 0:
+            assert h == 0 and not q.any()
+            continue
+        assert np.all(np.abs(vals[b] / d - q) <= 0.5)
+        assert np.abs(q[np.argmax(np.abs(vals[b]))]) == 127
+
+
+def test_quant_ties_round_toward_plus_infinity():
+    # amax 127 makes d exactly 1, so v / d are the values themselves. JS
+    # Math.round sends x.5 up: 2.5 -> 3, -2.5 -> -2, 0.5 -> 1, -0.5 -> 0.
+    v = np.zeros(32, np.float32)
+    v[:6] = [127, 2.5, -2.5, 0.5, -0.5, -127]
+    q = oracle.quant_matrix_q8(v, 1, 32)[2:].view(np.int8)
+    assert list(q[:6]) == [127, 3, -2, 1, 0, -127]
+
+
+def test_split_is_a_byte_permutation():
+    rows, cols = 3, 64
+    packed = np.arange(rows * cols // 32 * 34, dtype=np.int64).astype(np.uint8)
+    qs, sc = oracle.split_q8(packed, rows, cols)
+    blocks = packed.reshape(-1, 34)
+    assert np.array_equal(sc, blocks[:, 0].astype(np.uint16) | (blocks[:, 1].astype(np.uint16) << 8))
+    assert np.array_equal(qs.view(np.uint8), blocks[:, 2:].ravel())
+
+
+# ---------------------------------------------------------------- matvec
+def int_problem(rng, rows, cols, scale_bits=0x3C00):
+    """Integer quants, power-of-two scales, small integer x: every partial sum
+    is an integer well inside 2^24, so any summation order is exact."""
+    q = rng.integers(-128, 128, (rows, cols))
+    x = rng.integers(-8, 9, cols).astype(np.float32)
+    scales = np.full((rows, cols // 32), scale_bits, np.int64)
+    packed = b"".join(block(int(scales[r, b]), q[r, 32 * b:32 * b + 32])
+                      for r in range(rows) for b in range(cols // 32))
+    return np.frombuffer(packed, np.uint8), q, x, scales
+
+
+@pytest.mark.parametrize("lanes", [0, 64])
+@pytest.mark.parametrize("rows,cols", [(7, 32), (16, 1024), (4, 3072), (3, 8192)])
+def test_matvec_exact_on_integer_problems(lanes, rows, cols):
+    rng = np.random.default_rng(rows * cols + lanes)
+    packed, q, x, _ = int_problem(rng, rows, cols)
+    want = (q @ x.astype(np.int64)).astype(np.float32)
+    assert np.array_equal(oracle.q8_matvec(packed, x, rows, cols, lanes), want)
+
+
+def test_matvec_uses_each_blocks_own_scale():
+    # Scales 2^k per block (f16 exponent bits), integer data: still exact.
+    rng = np.random.default_rng(7)
+    rows, cols = 5, 256
+    q = rng.integers(-128, 128, (rows, cols))
+    x = rng.integers(-4, 5, cols).astype(np.float32)
+    k = rng.integers(-3, 4, (rows, cols // 32))
+    packed = np.frombuffer(b"".join(
+        block(int((15 + k[r, b]) << 10), q[r, 32 * b:32 * b + 32])
+        for r in range(rows) for b in range(cols // 32)), np.uint8)
+    w = q.astype(np.float64) * np.repeat(2.0 ** k, 32, axis=1)
+    want = (w @ x.astype(np.float64)).astype(np.float32)
+    for lanes in (0, 64):
+        assert np.array_equal(oracle.q8_matvec(packed, x, rows, cols, lanes), want)
+
+
+def test_matvec_coop_order_is_the_lane_tree():
+    # Hand-derived from q8_coop.wgsl / matmulF32: with 64 lanes, block b goes
+    # to lane b % 64 and the 64 partials meet in a pairwise tree. Lane 0 holds
+    # 2^24 (block 0), lane 1 holds -2^24 (block 1), lane 32 holds 1 (block 32).
+    # Tree: stride 32 rounds 2^24 + 1 back to 2^24 (ties to even), lanes 0 and
+    # 1 then cancel: result 0. Serial order (blocks 0, 1, ..., 32) gives 1.
+    cols = 33 * 32
+    q = np.zeros((1, cols), np.int64)
+    x = np.zeros(cols, np.float32)
+    q[0, 0], x[0] = 64, 2.0 ** 18
+    q[0, 32], x[32] = -64, 2.0 ** 18
+    q[0, 32 * 32], x[32 * 32] = 1, 1.0
+    packed = np.frombuffer(b"".join(block(0x3C00, q[0, 32 * b:32 * b + 32]) for b in range(33)),
+                           np.uint8)
+    assert oracle.q8_matvec(packed, x, 1, cols, 64)[0] == 0.0
+    assert oracle.q8_matvec(packed, x, 1, cols, 0)[0] == 1.0
+
+
+def test_matvec_within_f32_bound_of_f64():
+    rng = np.random.default_rng(11)
+    rows, cols = 64, 3072
+    w = (rng.standard_normal(rows * cols) * 0.05).astype(np.float32)
+    packed = oracle.quant_matrix_q8(w, rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    qs, sc = oracle.split_q8(packed, rows, cols)
+    deq = qs.astype(np.float64).reshape(rows, cols // 32, 32) * np.array(
+        [oracle.half_to_f32(int(h)) for h in sc], np.float64).reshape(rows, cols // 32, 1)
+    exact = deq.reshape(rows, cols) @ x.astype(np.float64)
+    mag = np.abs(deq.reshape(rows, cols)) @ np.abs(x.astype(np.float64))
+    for lanes in (0, 64):
+        got = oracle.q8_matvec(packed, x, rows, cols, lanes).astype(np.float64)
+        # Every term passes through at most ~cols/32 + 40 roundings of 2^-24.
+        assert np.all(np.abs(got - exact) <= (cols / 32 + 40) * 2.0 ** -24 * mag)
+
+
+def test_fused_and_two_rounding_fma_agree_on_typical_data():
+    # The reference's fma32 rounds twice; v_fma_f32 once. With int8 weights the
+    # f64 sums are exact in practice, so the two models give the same bits.
+    rng = np.random.default_rng(12)
+    rows, cols = 256, 1024
+    packed = oracle.quant_matrix_q8((rng.standard_normal(rows * cols) * 0.05).astype(np.float32),
+                                    rows, cols)
+    x = rng.standard_normal(cols).astype(np.float32)
+    a = oracle.q8_matvec(packed, x, rows, cols, 64, fused=False)
+    b = oracle.q8_matvec(packed, x, rows, cols, 64, fused=True)
+    assert np.array_equal(a, b)
