@@ -22,9 +22,13 @@ of the hot path over one batch of synthetic, HBM-resident input:
   copy       1 GiB device-to-device copy (torch): the reference kernel of
              known traffic that calibrates the FETCH_SIZE / WRITE_SIZE
              counters in profiles/.
+  q8lmhead   The Q8_0 projection next to the path at its largest: the
+             151936 x 1024 LM head, one token (flk_q8_matvec). GB/s.
+  q8proj     The seven Q8_0 projections of all 28 layers for one decode
+             token (196 flk_q8_matvec calls). GB/s.
 
 The default run also measures prefill2k (the metric's second half) and reports
-it under "prefill". Inputs are N(0, 1) from a seeded generator (gains
+it under "prefill", and the LM-head projection under "q8_lm_head". Inputs are N(0, 1) from a seeded generator (gains
 N(1, 0.1)); caches are written on the device before timing starts.
 
 Timing: HIP events recorded on the stream the kernels are launched on bracket
@@ -350,7 +354,111 @@ class Copy(Workload):
         return {"workload": f"device-to-device copy of {self.src.numel() * 4} bytes"}
 
 
-WORKLOADS = {c.name: c for c in (Decode32k, Prefill2k, Ragged, Chunk32k, Decode512, Copy)}
+class Q8LmHead(Workload):
+    """Qwen3-0.6B's tied LM head as one Q8_0 matvec: 151936 x 1024."""
+
+    name = "q8lmhead"
+    kernel = "flk_q8_matvec: q8_matvec_kernel<32,1> (coop(64) order, 2 rows per wave)"
+    rows, cols, copies = 151936, 1024, 3
+
+    def __init__(self, torch, ops):
+        self.torch, self.ops = torch, ops
+        g = torch.Generator(device="cuda")
+        g.manual_seed(151936)
+        n = self.rows * self.cols
+        # Three weight copies (496 MB) rotate so the 256 MB MALL cannot hold them.
+        self.qs = [torch.randint(-128, 128, (n,), device="cuda", generator=g, dtype=torch.int8)
+                   for _ in range(self.copies)]
+        self.sc = [(torch.rand(n // 32, device="cuda", generator=g) * 8e-4 + 1e-5)
+                   .to(torch.float16).view(torch.int16) for _ in range(self.copies)]
+        self.x = torch.randn(self.cols, device="cuda", generator=g)
+        self.o = torch.empty(self.rows, device="cuda")
+        self.work_per_call = self.rows * self.cols * 34 // 32 + 4 * (self.cols + self.rows)
+        self.work_per_step = self.work_per_call
+        self.calls_per_step = 1
+        self.i = 0
+
+    def call(self, l=0):
+        c = self.i % self.copies
+        self.i += 1
+        self.ops.q8_matvec(None, self.x, self.o, 1, qs=self.qs[c], scales=self.sc[c],
+                           n_rows=self.rows, n_cols=self.cols)
+
+    def step(self):
+        self.call()
+
+    def config(self):
+        return {"workload": f"Q8_0 matvec {self.rows} x {self.cols} (LM head), 1 token",
+                "rows": self.rows, "cols": self.cols, "weight_bytes": self.rows * self.cols * 34 // 32}
+
+    def cpu_baseline(self, seconds=10.0):
+        """oracle.q8_matvec (coop(64), 1 thread) on 4096-row slices, ~10 s."""
+        import oracle
+        rng = np.random.default_rng(9)
+        rows = 4096
+        blocks = np.empty((rows * self.cols // 32, 34), np.uint8)
+        blocks[:, :2] = (np.abs(rng.standard_normal(blocks.shape[0])) * 4e-4 + 1e-5).astype(
+            np.float16).view(np.uint8).reshape(-1, 2)
+        blocks[:, 2:] = rng.integers(0, 256, (blocks.shape[0], 32), dtype=np.uint8)
+        packed = blocks.ravel()
+        x = rng.standard_normal(self.cols).astype(np.float32)
+        n, t0 = 0, time.perf_counter()
+        while time.perf_counter() - t0 < seconds:
+            oracle.q8_matvec(packed, x, rows, self.cols, 64)
+            n += 1
+        dt = time.perf_counter() - t0
+        per = rows * self.cols * 34 // 32 + 4 * (self.cols + rows)
+        return {"value": round(n * per / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
+                "sample": f"{n} x oracle q8_matvec of a {rows} x {self.cols} slice (coop(64), "
+                          f"1 thread), {dt:.1f} s"}
+
+
+class Q8Proj(Workload):
+    """The seven Q8_0 projections of every Qwen3-0.6B layer, one decode token,
+    28 layers: q 2048x1024, k and v 1024x1024, o 1024x2048, gate and up
+    3072x1024, down 1024x3072."""
+
+    name = "q8proj"
+    kernel = "flk_q8_matvec (7 calls per layer; mean over the calls)"
+    shapes = [(2048, 1024), (1024, 1024), (1024, 1024), (1024, 2048), (3072, 1024),
+              (3072, 1024), (1024, 3072)]
+    layers = 28
+
+    def __init__(self, torch, ops):
+        self.torch, self.ops = torch, ops
+        g = torch.Generator(device="cuda")
+        g.manual_seed(28)
+        self.w = []
+        for _ in range(self.layers):
+            for r, c in self.shapes:
+                qs = torch.randint(-128, 128, (r * c,), device="cuda", generator=g, dtype=torch.int8)
+                sc = (torch.rand(r * c // 32, device="cuda", generator=g) * 8e-4 + 1e-5).to(
+                    torch.float16).view(torch.int16)
+                self.w.append((qs, sc, r, c))
+        self.x = torch.randn(3072, device="cuda", generator=g)
+        self.o = torch.empty(3072, device="cuda")
+        per = [r * c * 34 // 32 + 4 * (r + c) for r, c in self.shapes]
+        self.work_per_step = self.layers * sum(per)
+        self.calls_per_step = self.layers * len(self.shapes)
+        self.work_per_call = self.work_per_step / self.calls_per_step
+
+    def call(self, i):
+        qs, sc, r, c = self.w[i]
+        self.ops.q8_matvec(None, self.x, self.o, 1, qs=qs, scales=sc, n_rows=r, n_cols=c)
+
+    def step(self):
+        for i in range(self.calls_per_step):
+            self.call(i)
+
+    def config(self):
+        return {"workload": "Q8_0 projections of 28 Qwen3-0.6B layers (q, k, v, o, gate, up, "
+                            "down), 1 decode token", "layers": self.layers,
+                "shapes": self.shapes, "weight_bytes": self.layers * sum(
+                    r * c * 34 // 32 for r, c in self.shapes)}
+
+
+WORKLOADS = {c.name: c for c in (Decode32k, Prefill2k, Ragged, Chunk32k, Decode512, Copy,
+                                 Q8LmHead, Q8Proj)}
 
 
 def settle_clocks(torch, w, seconds=0.5):
@@ -418,7 +526,7 @@ def main():
     ap.add_argument("--workload", default="decode32k", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
-                    help="skip the prefill2k measurement of the default run")
+                    help="skip the prefill2k and q8lmhead measurements of the default run")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -448,11 +556,14 @@ def main():
             out["frac_of_hbm_peak"] = round(main_res["value"] / HBM_PEAK_GBS, 4)
         else:
             out["frac_of_fp32_mfma_peak"] = round(main_res["value"] / FP32_MFMA_PEAK_TFLOPS, 4)
-        pre_cpu = None
+        pre_cpu = q8_cpu = None
         if args.workload == "decode32k" and not args.no_secondary:
             p, pre_cpu = run(torch, ops, stream, "prefill2k", max(5, args.steps), args.warmup)
             p["frac_of_fp32_mfma_peak"] = round(p["value"] / FP32_MFMA_PEAK_TFLOPS, 4)
             out["prefill"] = p
+            q, q8_cpu = run(torch, ops, stream, "q8lmhead", max(5, args.steps), args.warmup)
+            q["frac_of_hbm_peak"] = round(q["value"] / HBM_PEAK_GBS, 4)
+            out["q8_lm_head"] = q
     # CPU baselines last, with the GPU measurements done.
     if not args.no_cpu_baseline:
         log(f"[{args.workload}] CPU baseline (oracle port, 1 thread)")
@@ -460,6 +571,9 @@ def main():
         if pre_cpu is not None:
             log("[prefill2k] CPU baseline (oracle port, 1 thread)")
             out["prefill"]["cpu_baseline"] = pre_cpu()
+        if q8_cpu is not None:
+            log("[q8lmhead] CPU baseline (oracle port, 1 thread)")
+            out["q8_lm_head"]["cpu_baseline"] = q8_cpu()
     print(json.dumps(out), flush=True)
 
 

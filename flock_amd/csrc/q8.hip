@@ -28,8 +28,14 @@ namespace flk {
 constexpr int kQ8Lanes = 64;      // the reference's LANES (q8_coop.wgsl:58)
 constexpr int kQ8Threads = 256;   // 4 waves
 // Row groups whose loads are in flight together (fewer when x takes more registers).
+#ifndef FLK_Q8_UNROLL
+#define FLK_Q8_UNROLL 4
+#endif
+#ifndef FLK_Q8_WG_PER_CU
+#define FLK_Q8_WG_PER_CU 0  // 0: as many as fit (occupancy query)
+#endif
 template <int NB>
-constexpr int q8_unroll() { return NB == 1 ? 4 : (NB == 2 ? 2 : 1); }
+constexpr int q8_unroll() { return NB == 1 ? FLK_Q8_UNROLL : (NB == 2 ? 2 : 1); }
 constexpr int kQ8MaxRegBlocks = 4;  // x blocks per lane kept in registers (8192 columns)
 
 struct Q8Args {
@@ -173,19 +179,39 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
   }
 }
 
-// Workgroups: enough waves to keep ~8 per SIMD busy, never more than there
+// Workgroups: one resident wave of them (every CU filled to its occupancy
+// limit, so no workgroup waits for another to finish), never more than there
 // are row groups.
-static uint32_t q8_grid_x(uint32_t n_groups, int unroll) {
-  const uint32_t per_wg = (kQ8Threads / kWave) * unroll;
+template <int P, int NB>
+static uint32_t q8_grid_x(uint32_t n_groups) {
+  static int per_cu = 0;
+  if (per_cu == 0) {
+    int n = 0;
+    if (FLK_Q8_WG_PER_CU > 0 ||
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, q8_matvec_kernel<P, NB>, kQ8Threads, 0) !=
+            hipSuccess ||
+        n < 1)
+      n = FLK_Q8_WG_PER_CU > 0 ? FLK_Q8_WG_PER_CU : 2;
+    per_cu = n;
+  }
+  static int cus_of[64] = {0};
+  int dev = 0, cus = 256;
+  if (hipGetDevice(&dev) == hipSuccess && dev >= 0 && dev < 64) {
+    if (cus_of[dev] == 0 &&
+        hipDeviceGetAttribute(&cus_of[dev], hipDeviceAttributeMultiprocessorCount, dev) != hipSuccess)
+      cus_of[dev] = 256;
+    cus = cus_of[dev];
+  }
+  const uint32_t per_wg = (kQ8Threads / kWave) * q8_unroll<NB>();
   const uint32_t need = (n_groups + per_wg - 1) / per_wg;
-  const uint32_t cap = 256 * 8;
+  const uint32_t cap = (uint32_t)(per_cu * cus);
   return need < cap ? (need > 0 ? need : 1) : cap;
 }
 
 template <int P, int NB>
 static void launch_q8(const Q8Args& a, hipStream_t st) {
   const uint32_t groups = (a.n_rows + (kWave / P) - 1) / (kWave / P);
-  hipLaunchKernelGGL((q8_matvec_kernel<P, NB>), dim3(q8_grid_x(groups, q8_unroll<NB>()), a.n_tokens),
+  hipLaunchKernelGGL((q8_matvec_kernel<P, NB>), dim3(q8_grid_x<P, NB>(groups), a.n_tokens),
                      dim3(kQ8Threads), 0, st, a);
 }
 
