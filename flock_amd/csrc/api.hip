@@ -381,6 +381,47 @@ int32_t flk_q8_matvec(const int8_t* qs, const uint16_t* scales, const float* x, 
                     "flk_q8_matvec");
 }
 
+// ------------------------------------------------------------------ head ---
+uint64_t flk_argmax_ws_bytes(uint32_t n) { return argmax_ws_bytes(n > 0 ? n : 1); }
+
+int32_t flk_argmax(const float* x, uint32_t n, float* oval, uint32_t* oidx, void* ws,
+                   uint64_t ws_bytes) {
+  FLK_NONNULL(x);
+  FLK_NONNULL(oval);
+  FLK_NONNULL(oidx);
+  if (n == 0) return fail(FLK_ERR_ARG, "argmax of an empty vector");
+  if (int32_t rc = check_ws(ws, ws_bytes, argmax_ws_bytes(n))) return rc;
+  return hip_status(launch_argmax(x, n, oval, oidx, ws, g_stream), "flk_argmax");
+}
+
+uint64_t flk_lm_head_ws_bytes(uint32_t vocab, uint32_t hidden) {
+  if (vocab == 0 || hidden == 0 || hidden % 32 != 0) return 0;
+  return lm_head_ws_bytes(vocab, hidden);
+}
+
+int32_t flk_lm_head(const float* x, const float* norm_gain, float eps, const int8_t* qs,
+                    const uint16_t* scales, uint32_t vocab, uint32_t hidden, float* normed,
+                    float* logits, float* oval, uint32_t* oidx, void* ws, uint64_t ws_bytes) {
+  FLK_NONNULL(x);
+  FLK_NONNULL(norm_gain);
+  FLK_NONNULL(qs);
+  FLK_NONNULL(scales);
+  FLK_NONNULL(normed);
+  FLK_NONNULL(oval);
+  FLK_NONNULL(oidx);
+  if (vocab == 0 || hidden == 0 || hidden % 32 != 0)
+    return fail(FLK_ERR_ARG, "lm_head vocab=%u hidden=%u (hidden a multiple of 32)", vocab, hidden);
+  if (!(eps >= 0.f)) return fail(FLK_ERR_ARG, "lm_head eps must be >= 0");
+  FLK_ALIGNED(qs);
+  FLK_ALIGNED(normed);
+  if (reinterpret_cast<uintptr_t>(scales) % 2 != 0)
+    return fail(FLK_ERR_ARG, "scales must be 2-byte aligned");
+  if (int32_t rc = check_ws(ws, ws_bytes, lm_head_ws_bytes(vocab, hidden))) return rc;
+  return hip_status(launch_lm_head(x, norm_gain, eps, reinterpret_cast<const uint8_t*>(qs), scales,
+                                   vocab, hidden, normed, logits, oval, oidx, ws, g_stream),
+                    "flk_lm_head");
+}
+
 // splitQ8, kernels/lib.ts:141-156 (host memory only).
 int32_t flk_q8_split(const uint8_t* packed, uint32_t n_rows, uint32_t n_cols, int8_t* qs,
                      uint16_t* scales) {

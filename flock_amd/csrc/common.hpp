@@ -191,9 +191,67 @@ hipError_t launch_prefill(const float* q, const float* kcache, const float* vcac
                           uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                           uint32_t n_queries, uint32_t pos0, void* ws, hipStream_t st);
 
+// ------------------------------------------------------------------ argmax --
+// argmax.wgsl's contract: (va, ia) beats (vb, ib) if va > vb, or va == vb and
+// ia < ib; the empty result is (-3.4028235e38, 0xffffffff), and a NaN never
+// wins (every comparison with it is false). The order of comparisons does not
+// change the result, so any reduction tree gives the reference's answer.
+constexpr float kArgmaxNoVal = -3.40282347e38f;
+constexpr uint32_t kArgmaxNoIdx = 0xffffffffu;
+
+__device__ __forceinline__ bool argmax_better(float va, uint32_t ia, float vb, uint32_t ib) {
+  return va > vb || (va == vb && ia < ib);
+}
+
+// Reduces every thread's (v, i) of the workgroup (blockDim.x a multiple of 64,
+// at most 1024) and writes the winner to val[blockIdx.x], idx[blockIdx.x].
+// Every thread of the workgroup must call it.
+__device__ __forceinline__ void argmax_block_store(float v, uint32_t i, float* val, uint32_t* idx) {
+  __shared__ float s_v[16];
+  __shared__ uint32_t s_i[16];
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) {
+    const float ov = __shfl_xor(v, m, kWave);
+    const uint32_t oi = (uint32_t)__shfl_xor((int)i, m, kWave);
+    if (argmax_better(ov, oi, v, i)) {
+      v = ov;
+      i = oi;
+    }
+  }
+  const int wave = threadIdx.x >> 6;
+  if ((threadIdx.x & 63) == 0) {
+    s_v[wave] = v;
+    s_i[wave] = i;
+  }
+  __syncthreads();
+  if (threadIdx.x == 0) {
+    for (int w = 1; w < (int)(blockDim.x >> 6); w++)
+      if (argmax_better(s_v[w], s_i[w], v, i)) {
+        v = s_v[w];
+        i = s_i[w];
+      }
+    val[blockIdx.x] = v;
+    idx[blockIdx.x] = i;
+  }
+}
+
 // ------------------------------------------------------------- Q8_0 matvec --
+// best_val / best_idx: per-workgroup argmax partials (null for a plain
+// matvec); *n_workgroups receives the launch's workgroup count.
 hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const float* x, float* o,
-                            uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, hipStream_t st);
+                            uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, hipStream_t st,
+                            float* best_val = nullptr, uint32_t* best_idx = nullptr,
+                            uint32_t* n_workgroups = nullptr);
+uint32_t q8_max_workgroups(uint32_t n_rows, uint32_t n_cols);
+
+// ------------------------------------------------------------------- head ----
+uint64_t argmax_ws_bytes(uint32_t n);
+hipError_t launch_argmax(const float* x, uint32_t n, float* oval, uint32_t* oidx, void* ws,
+                         hipStream_t st);
+uint64_t lm_head_ws_bytes(uint32_t vocab, uint32_t hidden);
+hipError_t launch_lm_head(const float* x, const float* gain, float eps, const uint8_t* qs,
+                          const uint16_t* scales, uint32_t vocab, uint32_t hidden, float* normed,
+                          float* logits, float* oval, uint32_t* oidx, void* ws, hipStream_t st);
 
 // Workspace layout (split-K partials): [(m, l) pairs][pad to 256 B][acc rows].
 constexpr uint64_t kWsAlign = 256;

@@ -42,8 +42,10 @@ struct Q8Args {
   const uint8_t* qs;
   const uint16_t* scales;
   const float* x;
-  float* o;
+  float* o;                 // may be null when best_val is set (argmax only)
   uint32_t n_rows, n_cols, n_tokens;
+  float* best_val;          // per-workgroup argmax partials (null: none)
+  uint32_t* best_idx;
 };
 
 // halfToF32 (kernels/lib.ts:28-33): exact for every finite f16 (subnormals
@@ -114,6 +116,10 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
     }
   }
 
+  // Running argmax over the rows this lane finishes (argmax.wgsl's sentinel).
+  float bv = kArgmaxNoVal;
+  uint32_t bi = kArgmaxNoIdx;
+
   const uint32_t n_groups = (a.n_rows + R - 1) / R;
   for (uint32_t g0 = wave; g0 < n_groups; g0 += waves * kQ8Unroll) {
     // Loads of kQ8Unroll row groups first (rows past the end re-read the last
@@ -142,10 +148,16 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
 #pragma unroll
       for (int m = P / 2; m >= 1; m >>= 1) part += shfl_xor(part, m);
       const uint32_t row = (g0 + waves * u) * R + sub;
-      if (ll == 0 && g0 + waves * u < n_groups && row < a.n_rows)
-        a.o[(size_t)tok * a.n_rows + row] = part;
+      if (ll == 0 && g0 + waves * u < n_groups && row < a.n_rows) {
+        if (a.o != nullptr) a.o[(size_t)tok * a.n_rows + row] = part;
+        if (argmax_better(part, row, bv, bi)) {
+          bv = part;
+          bi = row;
+        }
+      }
     }
   }
+  if (a.best_val != nullptr) argmax_block_store(bv, bi, a.best_val, a.best_idx);
 }
 
 // Columns past kQ8MaxRegBlocks * 64 blocks: the same arithmetic with x read
@@ -157,6 +169,8 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
   const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
   const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
   const float* xt = a.x + (size_t)tok * a.n_cols;
+  float bv = kArgmaxNoVal;
+  uint32_t bi = kArgmaxNoIdx;
   for (uint32_t row = wave; row < a.n_rows; row += waves) {
     float part = 0.f;
     for (uint32_t b = lane; b < nb; b += kQ8Lanes) {
@@ -175,8 +189,15 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) part += shfl_xor(part, m);
-    if (lane == 0) a.o[(size_t)tok * a.n_rows + row] = part;
+    if (lane == 0) {
+      if (a.o != nullptr) a.o[(size_t)tok * a.n_rows + row] = part;
+      if (argmax_better(part, row, bv, bi)) {
+        bv = part;
+        bi = row;
+      }
+    }
   }
+  if (a.best_val != nullptr) argmax_block_store(bv, bi, a.best_val, a.best_idx);
 }
 
 // Workgroups: one resident wave of them (every CU filled to its occupancy
@@ -209,41 +230,57 @@ static uint32_t q8_grid_x(uint32_t n_groups) {
 }
 
 template <int P, int NB>
-static void launch_q8(const Q8Args& a, hipStream_t st) {
+static uint32_t launch_q8(const Q8Args& a, hipStream_t st) {
   const uint32_t groups = (a.n_rows + (kWave / P) - 1) / (kWave / P);
-  hipLaunchKernelGGL((q8_matvec_kernel<P, NB>), dim3(q8_grid_x<P, NB>(groups), a.n_tokens),
-                     dim3(kQ8Threads), 0, st, a);
+  const uint32_t gx = q8_grid_x<P, NB>(groups);
+  hipLaunchKernelGGL((q8_matvec_kernel<P, NB>), dim3(gx, a.n_tokens), dim3(kQ8Threads), 0, st, a);
+  return gx;
+}
+
+// Row groups of the register-x kernel and the workgroups it launches at most
+// (the argmax partials of flk_lm_head need one slot per workgroup).
+uint32_t q8_max_workgroups(uint32_t n_rows, uint32_t n_cols) {
+  const uint32_t nb = n_cols / 32;
+  uint32_t P = 1;
+  while (P < nb && P < 64) P <<= 1;
+  const uint32_t groups = (n_rows + (kWave / P) - 1) / (kWave / P);
+  const uint32_t ub = nb > 128 ? 1 : (nb > 64 ? 2 : FLK_Q8_UNROLL);
+  const uint32_t per_wg = (kQ8Threads / kWave) * ub;
+  return (groups + per_wg - 1) / per_wg;
 }
 
 hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const float* x, float* o,
                             uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
-                            hipStream_t st) {
-  Q8Args a{qs, scales, x, o, n_rows, n_cols, n_tokens};
+                            hipStream_t st, float* best_val, uint32_t* best_idx,
+                            uint32_t* n_workgroups) {
+  Q8Args a{qs, scales, x, o, n_rows, n_cols, n_tokens, best_val, best_idx};
   const uint32_t nb = n_cols / 32;
+  uint32_t gx;
   if (nb > (uint32_t)kQ8Lanes * kQ8MaxRegBlocks) {
-    const uint32_t wg = (n_rows + 3) / 4 < 2048u ? (n_rows + 3) / 4 : 2048u;
-    hipLaunchKernelGGL(q8_matvec_wide_kernel, dim3(wg, n_tokens), dim3(kQ8Threads), 0, st, a);
+    gx = (n_rows + 3) / 4 < 2048u ? (n_rows + 3) / 4 : 2048u;
+    hipLaunchKernelGGL(q8_matvec_wide_kernel, dim3(gx, n_tokens), dim3(kQ8Threads), 0, st, a);
   } else if (nb > 192) {
-    launch_q8<64, 4>(a, st);
+    gx = launch_q8<64, 4>(a, st);
   } else if (nb > 128) {
-    launch_q8<64, 3>(a, st);
+    gx = launch_q8<64, 3>(a, st);
   } else if (nb > 64) {
-    launch_q8<64, 2>(a, st);
+    gx = launch_q8<64, 2>(a, st);
   } else if (nb > 32) {
-    launch_q8<64, 1>(a, st);
+    gx = launch_q8<64, 1>(a, st);
   } else if (nb > 16) {
-    launch_q8<32, 1>(a, st);
+    gx = launch_q8<32, 1>(a, st);
   } else if (nb > 8) {
-    launch_q8<16, 1>(a, st);
+    gx = launch_q8<16, 1>(a, st);
   } else if (nb > 4) {
-    launch_q8<8, 1>(a, st);
+    gx = launch_q8<8, 1>(a, st);
   } else if (nb > 2) {
-    launch_q8<4, 1>(a, st);
+    gx = launch_q8<4, 1>(a, st);
   } else if (nb > 1) {
-    launch_q8<2, 1>(a, st);
+    gx = launch_q8<2, 1>(a, st);
   } else {
-    launch_q8<1, 1>(a, st);
+    gx = launch_q8<1, 1>(a, st);
   }
+  if (n_workgroups != nullptr) *n_workgroups = gx;
   return hipGetLastError();
 }
 

@@ -237,3 +237,29 @@ def q8_matvec(w, x, o, n_tokens: int = 1, qs=None, scales=None, n_rows: int | No
         qs, scales, n_rows, n_cols = w.qs, w.scales, w.rows, w.cols
     check(lib().flk_q8_matvec(ptr(qs), ptr(scales), ptr(x), ptr(o), n_rows, n_cols, n_tokens),
           "flk_q8_matvec")
+
+
+# ---------------------------------------------------------------- the head
+def argmax_ws_bytes(n: int) -> int:
+    return int(lib().flk_argmax_ws_bytes(n))
+
+
+def argmax(x, n: int, oval, oidx, ws) -> None:
+    """argmax.wgsl pass1 + pass2 (model.ts:337-346): largest value, lowest index."""
+    w, nb = _ws(ws)
+    check(lib().flk_argmax(ptr(x), n, ptr(oval), ptr(oidx), w, nb), "flk_argmax")
+
+
+def lm_head_ws_bytes(vocab: int, hidden: int) -> int:
+    return int(lib().flk_lm_head_ws_bytes(vocab, hidden))
+
+
+def lm_head(x, gain, eps: float, w: "Q8Matrix", normed, logits, oval, oidx, ws) -> None:
+    """encodeHead (model.ts:307-346): rmsnorm -> tied Q8_0 projection -> argmax.
+
+    ``w`` is the vocab x hidden matrix; ``logits`` may be None.
+    """
+    wsp, nb = _ws(ws)
+    check(lib().flk_lm_head(ptr(x), ptr(gain), eps, ptr(w.qs), ptr(w.scales), w.rows, w.cols,
+                            ptr(normed), ptr(logits), ptr(oval), ptr(oidx), wsp, nb),
+          "flk_lm_head")

@@ -38,6 +38,29 @@ int32_t flk_q8_matvec(const int8_t* qs, const uint16_t* scales, const float* x, 
 int32_t flk_q8_split(const uint8_t* packed, uint32_t n_rows, uint32_t n_cols, int8_t* qs,
                      uint16_t* scales);
 
+/* ---- the head after the last layer (model.ts:307-346, encodeHead) ---- */
+
+/* Greedy token: replaces argmax.wgsl pass1 + pass2 (model.ts:337-346).
+ * *oval, *oidx (device) receive the largest x[i] and the lowest index holding
+ * it; NaN is never chosen; if nothing beats -3.4028235e38 the result is
+ * (-3.4028235e38, 0xffffffff), exactly as argmax.wgsl. ws: device workspace
+ * of flk_argmax_ws_bytes(n) bytes, 256-byte aligned (argmax.wgsl's
+ * amVal/amIdx partial buffers). */
+uint64_t flk_argmax_ws_bytes(uint32_t n);
+int32_t flk_argmax(const float* x, uint32_t n, float* oval, uint32_t* oidx, void* ws,
+                   uint64_t ws_bytes);
+
+/* encodeHead (model.ts:307-346) in one call: normed = rmsnorm(x[hidden],
+ * norm_gain, eps) (rmsnorm.wgsl, one vector), logits = W normed with W the
+ * vocab x hidden Q8_0 matrix (the tied token_embd), then the argmax of the
+ * logits into *oval, *oidx as flk_argmax. logits may be NULL (greedy decode
+ * needs only the token); when given it receives what flk_q8_matvec would
+ * write. ws: flk_lm_head_ws_bytes(vocab, hidden) bytes, 256-byte aligned. */
+uint64_t flk_lm_head_ws_bytes(uint32_t vocab, uint32_t hidden);
+int32_t flk_lm_head(const float* x, const float* norm_gain, float eps, const int8_t* qs,
+                    const uint16_t* scales, uint32_t vocab, uint32_t hidden, float* normed,
+                    float* logits, float* oval, uint32_t* oidx, void* ws, uint64_t ws_bytes);
+
 #ifdef __cplusplus
 }
 #endif

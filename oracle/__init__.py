@@ -74,6 +74,7 @@ def lib() -> ctypes.CDLL:
             "flko_quant_row_q8": (None, [_f32p, i64, _u8p]),
             "flko_split_q8": (None, [_u8p, i, i, _u8p, _u8p]),
             "flko_q8_matvec": (None, [_u8p, _f32p, i, i, i, i, _f32p]),
+            "flko_argmax_wgsl": (None, [_f32p, i64, _f32p, ctypes.POINTER(ctypes.c_uint32)]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -279,3 +280,24 @@ def q8_matvec(packed, x, rows: int, cols: int, lanes: int = 64, fused: bool = Fa
         lib().flko_q8_matvec(_pu8(packed), _p(xt), rows, cols, lanes, int(bool(fused)), _p(ot))
         out[t * rows:(t + 1) * rows] = ot
     return out
+
+
+def argmax_wgsl(x):
+    """argmax.wgsl (kernels/argmax.wgsl:54-56, 92-134): (value, index) of the
+    largest element, lowest index among equal values, NaN never chosen,
+    (-3.4028235e38, 0xffffffff) when nothing beats that."""
+    x = _f32(x).ravel()
+    v = np.empty(1, np.float32)
+    i = np.empty(1, np.uint32)
+    lib().flko_argmax_wgsl(_p(x), x.size, _p(v), i.ctypes.data_as(ctypes.POINTER(ctypes.c_uint32)))
+    return float(v[0]), int(i[0])
+
+
+def lm_head(x, gain, eps: float, packed, vocab: int, hidden: int):
+    """encodeHead, kernels/model.ts:307-346: rmsnorm (rmsnorm.wgsl, one vector)
+    -> Q8_0 vocab projection (coop(64)) -> argmax.wgsl.
+    Returns (normed, logits, value, index)."""
+    normed = rmsnorm(x, gain, hidden, 1, eps)
+    logits = q8_matvec(packed, normed, vocab, hidden, 64, fused=True)
+    v, i = argmax_wgsl(logits)
+    return normed, logits, v, i

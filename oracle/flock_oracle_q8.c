@@ -22,6 +22,8 @@
  *                        product then three fma32), part[lane] =
  *                        fma32(scale, fr(d0 + d1), part[lane]); then the
  *                        pairwise treeSum (lib.ts:312-318).
+ *   flko_argmax_wgsl     argmax.wgsl's two-pass contract (lowest index among
+ *                        equal maxima, NaN never chosen, empty sentinel).
  *
  * `fused` selects the FMA model: 0 = the reference's fma32 (f64 a*b + c,
  * then rounded to f32: two roundings), 1 = fmaf (one rounding, what the GPU's
@@ -35,7 +37,9 @@
  * the double d, JS tie rule on constructed ties, amax -> +-127); matvec
  * against exact integer arithmetic on integer inputs (every order gives the
  * exact sum, so a wrong index or operand fails), against an f64 sum within
- * the f32 error bound, and coop against serial on integer inputs.
+ * the f32 error bound, and coop against serial on integer inputs;
+ * argmax_wgsl against numpy's argmax / nanargmax (lowest index of the
+ * maximum) and hand-derived sentinel cases.
  */
 #include <math.h>
 #include <stdint.h>
@@ -166,4 +170,22 @@ void flko_q8_matvec(const uint8_t* packed, const float* x, int rows, int cols, i
       out[r] = part[0];
     }
   }
+}
+
+/* argmax.wgsl's contract (kernels/argmax.wgsl:54-56, 92-134): (va, ia) beats
+ * (vb, ib) if va > vb or (va == vb and ia < ib); start from
+ * (-3.4028235e38, 0xffffffff). The comparison is a total order on non-NaN
+ * pairs, so the scan order does not matter; NaN never wins. argmaxRef
+ * (head_ref.ts:65-74) agrees on every input without NaN and with some value
+ * >= -3.4028235e38. */
+void flko_argmax_wgsl(const float* x, int64_t n, float* oval, uint32_t* oidx) {
+  float bv = -3.40282347e38f;
+  uint32_t bi = 0xffffffffu;
+  for (int64_t i = 0; i < n; i++)
+    if (x[i] > bv || (x[i] == bv && (uint32_t)i < bi)) {
+      bv = x[i];
+      bi = (uint32_t)i;
+    }
+  *oval = bv;
+  *oidx = bi;
 }

@@ -112,3 +112,79 @@ def test_integer_problem_is_exact(rng):
         for r in range(rows) for b in range(cols // 32)), np.uint8)
     got = run_gpu(packed, x, rows, cols)
     assert np.array_equal(got, (q @ x.astype(np.int64)).astype(np.float32))
+
+
+# ---------------------------------------------------------------- argmax / head
+def gpu_argmax(x):
+    n = x.size
+    xb = ops.DeviceBuffer.from_array(np.ascontiguousarray(x, np.float32))
+    ov, oi = ops.DeviceBuffer(4), ops.DeviceBuffer(4)
+    ws = ops.DeviceBuffer(ops.argmax_ws_bytes(n))
+    ops.argmax(xb, n, ov, oi, ws)
+    ops.sync()
+    return float(ov.download(1)[0]), int(oi.download(1, np.uint32)[0])
+
+
+@pytest.mark.parametrize("n", [1, 100, 256, 257, 4096, 151936, 1 << 20])
+def test_argmax_matches_oracle(rng, n):
+    x = rng.standard_normal(n).astype(np.float32)
+    assert gpu_argmax(x) == oracle.argmax_wgsl(x)
+
+
+def test_argmax_ties_nan_and_sentinel(rng):
+    n = 151936
+    x = rng.standard_normal(n).astype(np.float32)
+    top = float(x.max()) + 1.0
+    for i in (90000, 1234, 150000, 70001):  # equal maxima in different workgroups
+        x[i] = top
+    assert gpu_argmax(x) == (top, 1234) == oracle.argmax_wgsl(x)
+    x[5] = np.nan
+    x[1233] = np.nan
+    assert gpu_argmax(x) == oracle.argmax_wgsl(x) == (top, 1234)
+    y = np.full(1000, -np.inf, np.float32)
+    y[::7] = np.nan
+    assert gpu_argmax(y) == oracle.argmax_wgsl(y) == (-np.finfo(np.float32).max, 0xFFFFFFFF)
+    y[400] = -np.finfo(np.float32).max
+    assert gpu_argmax(y) == oracle.argmax_wgsl(y)
+
+
+def run_head(x, gain, packed, vocab, hidden, with_logits=True):
+    w = ops.Q8Matrix.from_packed(packed, vocab, hidden)
+    xb = ops.DeviceBuffer.from_array(x)
+    gb = ops.DeviceBuffer.from_array(gain)
+    normed = ops.DeviceBuffer(hidden * 4)
+    logits = ops.DeviceBuffer(vocab * 4) if with_logits else None
+    ov, oi = ops.DeviceBuffer(4), ops.DeviceBuffer(4)
+    ws = ops.DeviceBuffer(ops.lm_head_ws_bytes(vocab, hidden))
+    ops.lm_head(xb, gb, oracle.QWEN3_EPS, w, normed, logits, ov, oi, ws)
+    ops.sync()
+    return (normed.download(hidden), logits.download(vocab) if with_logits else None,
+            float(ov.download(1)[0]), int(oi.download(1, np.uint32)[0]))
+
+
+@pytest.mark.parametrize("vocab,hidden", [(151936, 1024), (1000, 64), (5003, 2048), (300, 8224)])
+def test_lm_head_matches_oracle(rng, vocab, hidden):
+    packed = random_packed(rng, vocab, hidden)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    gain = rng.normal(1, 0.1, hidden).astype(np.float32)
+    normed, logits, v, i = run_head(x, gain, packed, vocab, hidden)
+    w_normed, w_logits, w_v, w_i = oracle.lm_head(x, gain, oracle.QWEN3_EPS, packed, vocab, hidden)
+    assert np.array_equal(normed, w_normed)
+    assert np.array_equal(logits, w_logits)
+    assert (v, i) == (w_v, w_i)
+    # Without a logits buffer: the same token.
+    assert run_head(x, gain, packed, vocab, hidden, with_logits=False)[2:] == (w_v, w_i)
+
+
+def test_lm_head_tie_picks_lowest_row(rng):
+    vocab, hidden = 151936, 1024
+    packed = random_packed(rng, vocab, hidden).reshape(vocab, -1)
+    x = rng.standard_normal(hidden).astype(np.float32)
+    gain = np.ones(hidden, np.float32)
+    _, logits, _, m = oracle.lm_head(x, gain, oracle.QWEN3_EPS, packed.ravel(), vocab, hidden)
+    for r in (3, m // 2, vocab - 1):  # identical rows give identical logits
+        packed[r] = packed[m]
+    want = oracle.lm_head(x, gain, oracle.QWEN3_EPS, packed.ravel(), vocab, hidden)
+    assert want[3] == min(3, m)
+    got = run_head(x, gain, packed.ravel(), vocab, hidden)
+    assert got[2:] == want[2:]

@@ -183,3 +183,29 @@ def test_fused_and_two_rounding_fma_agree_on_typical_data():
     a = oracle.q8_matvec(packed, x, rows, cols, 64, fused=False)
     b = oracle.q8_matvec(packed, x, rows, cols, 64, fused=True)
     assert np.array_equal(a, b)
+
+
+# ---------------------------------------------------------------- argmax
+def test_argmax_wgsl_matches_numpy_lowest_index():
+    rng = np.random.default_rng(13)
+    for n in (1, 7, 256, 151936):
+        x = rng.standard_normal(n).astype(np.float32)
+        v, i = oracle.argmax_wgsl(x)
+        assert i == int(np.argmax(x)) and v == x[i]
+        assert i == oracle.argmax(x)  # argmaxRef (head_ref.ts:65-74) agrees on finite input
+    # Ties: several equal maxima, including -0 / +0 (equal under ==).
+    x = np.array([1, 5, 2, 5, 5, 0], np.float32)
+    assert oracle.argmax_wgsl(x) == (5.0, 1)
+    x = np.array([-1, -0.0, 0.0, -2], np.float32)
+    assert oracle.argmax_wgsl(x)[1] == 1
+
+
+def test_argmax_wgsl_nan_and_sentinel():
+    x = np.array([np.nan, 2, np.nan, 3, 3], np.float32)
+    assert oracle.argmax_wgsl(x) == (3.0, 3)
+    assert oracle.argmax_wgsl(x)[1] == int(np.nanargmax(x))
+    # Nothing beats the start value: argmax.wgsl returns its sentinel.
+    v, i = oracle.argmax_wgsl(np.array([-np.inf, np.nan], np.float32))
+    assert i == 0xFFFFFFFF and v == -F32_MAX
+    # -FLT_MAX itself wins (equal to the start value, lower index).
+    assert oracle.argmax_wgsl(np.array([-np.inf, -F32_MAX], np.float32))[1] == 1
