@@ -61,6 +61,9 @@ SIGNATURES: dict[str, tuple] = {
     # include/flock_q8.h
     "flk_q8_matvec": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32]),
     "flk_q8_split": (_i32, [_p, _u32, _u32, _p, _p]),
+    "flk_q8_matvec_ex": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32, _p, _f32, _p, _p]),
+    "flk_swiglu": (_i32, [_p, _p, _p, _u32]),
+    "flk_add": (_i32, [_p, _p, _p, _u32]),
     "flk_argmax_ws_bytes": (_u64, [_u32]),
     "flk_argmax": (_i32, [_p, _u32, _p, _p, _p, _u64]),
     "flk_lm_head_ws_bytes": (_u64, [_u32, _u32]),

@@ -422,6 +422,53 @@ int32_t flk_lm_head(const float* x, const float* norm_gain, float eps, const int
                     "flk_lm_head");
 }
 
+int32_t flk_q8_matvec_ex(const int8_t* qs, const uint16_t* scales, const float* x, float* o,
+                         uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
+                         const float* norm_gain, float norm_eps, const float* up,
+                         const float* res) {
+  FLK_NONNULL(qs);
+  FLK_NONNULL(scales);
+  FLK_NONNULL(x);
+  FLK_NONNULL(o);
+  if (n_rows == 0 || n_cols == 0 || n_tokens == 0)
+    return fail(FLK_ERR_ARG, "q8_matvec n_rows=%u n_cols=%u n_tokens=%u", n_rows, n_cols,
+                n_tokens);
+  if (n_cols % 32 != 0) return fail(FLK_ERR_ARG, "q8_matvec n_cols %u is not a multiple of 32", n_cols);
+  if (n_tokens > 65535) return fail(FLK_ERR_UNSUPPORTED, "q8_matvec n_tokens %u > 65535", n_tokens);
+  if (norm_gain != nullptr && up != nullptr)
+    return fail(FLK_ERR_ARG, "q8_matvec_ex: norm_gain and up are exclusive");
+  if (norm_gain != nullptr && !(norm_eps >= 0.f))
+    return fail(FLK_ERR_ARG, "q8_matvec_ex: eps must be >= 0");
+  FLK_ALIGNED(qs);
+  FLK_ALIGNED(x);
+  if (reinterpret_cast<uintptr_t>(scales) % 2 != 0)
+    return fail(FLK_ERR_ARG, "scales must be 2-byte aligned");
+  Q8Fuse f;
+  f.norm_gain = norm_gain;
+  f.norm_eps = norm_eps;
+  f.up = up;
+  f.res = res;
+  return hip_status(launch_q8_matvec(reinterpret_cast<const uint8_t*>(qs), scales, x, o, n_rows,
+                                     n_cols, n_tokens, g_stream, nullptr, nullptr, nullptr, &f),
+                    "flk_q8_matvec_ex");
+}
+
+int32_t flk_swiglu(const float* gate, const float* up, float* o, uint32_t n) {
+  FLK_NONNULL(gate);
+  FLK_NONNULL(up);
+  FLK_NONNULL(o);
+  if (n == 0) return fail(FLK_ERR_ARG, "swiglu of 0 elements");
+  return hip_status(launch_elementwise(0, gate, up, o, n, g_stream), "flk_swiglu");
+}
+
+int32_t flk_add(const float* a, const float* b, float* o, uint32_t n) {
+  FLK_NONNULL(a);
+  FLK_NONNULL(b);
+  FLK_NONNULL(o);
+  if (n == 0) return fail(FLK_ERR_ARG, "add of 0 elements");
+  return hip_status(launch_elementwise(1, a, b, o, n, g_stream), "flk_add");
+}
+
 // splitQ8, kernels/lib.ts:141-156 (host memory only).
 int32_t flk_q8_split(const uint8_t* packed, uint32_t n_rows, uint32_t n_cols, int8_t* qs,
                      uint16_t* scales) {

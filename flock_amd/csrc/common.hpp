@@ -238,11 +238,21 @@ __device__ __forceinline__ void argmax_block_store(float v, uint32_t i, float* v
 // ------------------------------------------------------------- Q8_0 matvec --
 // best_val / best_idx: per-workgroup argmax partials (null for a plain
 // matvec); *n_workgroups receives the launch's workgroup count.
+struct Q8Fuse {
+  const float* norm_gain = nullptr;  // x <- rmsnorm(x) (per token, n = n_cols)
+  float norm_eps = 0.f;
+  const float* up = nullptr;         // x <- swiglu(x, up)
+  const float* res = nullptr;        // o <- res + W x
+};
 hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const float* x, float* o,
                             uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, hipStream_t st,
                             float* best_val = nullptr, uint32_t* best_idx = nullptr,
-                            uint32_t* n_workgroups = nullptr);
+                            uint32_t* n_workgroups = nullptr, const Q8Fuse* fuse = nullptr);
 uint32_t q8_max_workgroups(uint32_t n_rows, uint32_t n_cols);
+
+// op 0: swiglu(a, b); op 1: a + b (elementwise.wgsl).
+hipError_t launch_elementwise(int op, const float* a, const float* b, float* o, uint32_t n,
+                              hipStream_t st);
 
 // ------------------------------------------------------------------- head ----
 uint64_t argmax_ws_bytes(uint32_t n);

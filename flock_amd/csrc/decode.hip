@@ -146,9 +146,19 @@ __device__ __forceinline__ void attend_keys(const float4 (&kr_in)[U], const floa
   for (int u = 0; u < U; u++) {
     const uint32_t t = base + u * PH + ph;
     const bool mine = owns_pos && t == pos;
-    kr[u] = mine ? knew : kr_in[u];
-    vr[u] = mine ? vnew : vr_in[u];
     const bool valid = t < t1;
+    kr[u] = mine ? knew : kr_in[u];
+    // A key past the end re-read row t1 - 1; its weight is exactly 0, but
+    // 0 * v is NaN if that row holds a NaN pattern -- and in the fused layer
+    // call row t1 - 1 is the row being appended in this launch, so other
+    // workgroups may read it before it is written. Such v are zeroed (a bit
+    // mask, so the row's contents never reach the sum).
+    const uint32_t keep = valid ? 0xffffffffu : 0u;
+    const float4 vv = mine ? vnew : vr_in[u];
+    vr[u] = make_float4(__uint_as_float(__float_as_uint(vv.x) & keep),
+                        __uint_as_float(__float_as_uint(vv.y) & keep),
+                        __uint_as_float(__float_as_uint(vv.z) & keep),
+                        __uint_as_float(__float_as_uint(vv.w) & keep));
 #pragma unroll
     for (int g = 0; g < G; g++) {
       float d = qv[g].x * kr[u].x;

@@ -50,6 +50,28 @@ __global__ __launch_bounds__(kArgmaxThreads) void argmax_final_kernel(
   argmax_block_store(bv, bi, oval, oidx);  // blockIdx.x == 0
 }
 
+// ------------------------------------------------------------- elementwise --
+// elementwise.wgsl:24-37, one thread per element. swiglu's exp is the f64 one
+// rounded to f32, as swigluRef (ops_ref.ts:103-110) computes it.
+__global__ __launch_bounds__(256) void elementwise_kernel(int op, const float* a, const float* b,
+                                                          float* o, uint32_t n) {
+  const uint32_t i = blockIdx.x * 256 + threadIdx.x;
+  if (i >= n) return;
+  const float g = a[i];
+  if (op == 0) {
+    const float e = (float)exp(-(double)g);
+    o[i] = (g / (1.f + e)) * b[i];
+  } else {
+    o[i] = g + b[i];
+  }
+}
+
+hipError_t launch_elementwise(int op, const float* a, const float* b, float* o, uint32_t n,
+                              hipStream_t st) {
+  hipLaunchKernelGGL(elementwise_kernel, dim3((n + 255) / 256), dim3(256), 0, st, op, a, b, o, n);
+  return hipGetLastError();
+}
+
 static uint32_t argmax_groups(uint32_t n) {
   const uint32_t g = (n + kArgmaxThreads - 1) / kArgmaxThreads;
   return g < kArgmaxMaxGroups ? (g > 0 ? g : 1) : kArgmaxMaxGroups;

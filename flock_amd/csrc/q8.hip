@@ -46,7 +46,48 @@ struct Q8Args {
   uint32_t n_rows, n_cols, n_tokens;
   float* best_val;          // per-workgroup argmax partials (null: none)
   uint32_t* best_idx;
+  // Input and output fusions (all null: plain W x):
+  const float* norm_gain;   // x <- rmsnorm(x) with this gain (rmsnorm.wgsl:41-73), eps below
+  float norm_eps;
+  const float* up;          // x <- swiglu(x, up) (elementwise.wgsl:24-30; x is the gate)
+  const float* res;         // o <- res + W x (elementwise.wgsl:32-37, the residual add)
 };
+
+// The matvec input element i of token tok after the optional fusion:
+// rmsnorm: fr(fr(x * scale) * g) (rmsnorm.wgsl:67-72); swiglu:
+// fr(fr(g / fr(1 + fr(exp(-g)))) * up) with exp in f64 and rounded once
+// (swigluRef, ops_ref.ts:103-110).
+__device__ __forceinline__ float q8_xin(const Q8Args& a, const float* xt, size_t tok_off,
+                                        uint32_t i, float scale) {
+  const float v = xt[i];
+  if (a.norm_gain != nullptr) return (v * scale) * a.norm_gain[i];
+  if (a.up != nullptr) {
+    const float e = (float)exp(-(double)v);
+    return (v / (1.f + e)) * a.up[tok_off + i];
+  }
+  return v;
+}
+
+// rmsnorm scale of token tok's x (rmsnorm.wgsl:45-66): 128 strided fma32
+// partials, pairwise LDS tree, scale = 1 / sqrt(mean + eps) rounded once. Every
+// thread of the workgroup must call it; returns 1 when there is no norm.
+__device__ __forceinline__ float q8_norm_scale(const Q8Args& a, const float* xt) {
+  if (a.norm_gain == nullptr) return 1.f;
+  __shared__ float part[128];
+  const uint32_t t = threadIdx.x;
+  if (t < 128) {
+    float acc = 0.f;
+    for (uint32_t i = t; i < a.n_cols; i += 128) acc = fma32(xt[i], xt[i], acc);
+    part[t] = acc;
+  }
+  __syncthreads();
+  for (uint32_t stride = 64; stride > 0; stride >>= 1) {
+    if (t < stride) part[t] = part[t] + part[t + stride];
+    __syncthreads();
+  }
+  const float mean = part[0] / (float)a.n_cols;
+  return rsqrt_once(mean + a.norm_eps);
+}
 
 // halfToF32 (kernels/lib.ts:28-33): exact for every finite f16 (subnormals
 // included); exponent 31 (inf, nan) becomes +-3.4028235e38, the largest f32.
@@ -85,7 +126,8 @@ __device__ __forceinline__ float q8_block(float part, float scale, uint4 w0, uin
 
 // P logical lanes per row, NB x blocks per lane in registers (NB * 64 >= the
 // row's block count). Grid: (workgroups over row groups, tokens).
-template <int P, int NB>
+// FUSE: the input fusions (rmsnorm / swiglu) are compiled in.
+template <int P, int NB, bool FUSE>
 __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
   constexpr int R = kWave / P;  // rows per wave per step
   constexpr int kQ8Unroll = q8_unroll<NB>();
@@ -97,22 +139,31 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
   const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
   const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
 
-  // x blocks ll, ll + 64, ... of this token (zeros past the row's end).
+  // x blocks ll, ll + 64, ... of this token (zeros past the row's end),
+  // after the optional input fusion.
+  const size_t tok_off = (size_t)tok * a.n_cols;
+  const float* xt = a.x + tok_off;
+  const float scale = FUSE ? q8_norm_scale(a, xt) : 1.f;
   float xr[NB][32];
   bool live[NB];
 #pragma unroll
   for (int j = 0; j < NB; j++) {
     const uint32_t b = ll + kQ8Lanes * j;
     live[j] = b < nb;
-    const float4* xs = reinterpret_cast<const float4*>(a.x + (size_t)tok * a.n_cols +
-                                                       32 * (size_t)min(b, nb - 1));
+    const uint32_t c0 = 32 * min(b, nb - 1);
+    if (!FUSE) {
+      const float4* xs = reinterpret_cast<const float4*>(xt + c0);
 #pragma unroll
-    for (int i = 0; i < 8; i++) {
-      const float4 v = xs[i];
-      xr[j][4 * i + 0] = v.x;
-      xr[j][4 * i + 1] = v.y;
-      xr[j][4 * i + 2] = v.z;
-      xr[j][4 * i + 3] = v.w;
+      for (int i = 0; i < 8; i++) {
+        const float4 v = xs[i];
+        xr[j][4 * i + 0] = v.x;
+        xr[j][4 * i + 1] = v.y;
+        xr[j][4 * i + 2] = v.z;
+        xr[j][4 * i + 3] = v.w;
+      }
+    } else {
+#pragma unroll
+      for (int i = 0; i < 32; i++) xr[j][i] = q8_xin(a, xt, tok_off, c0 + i, scale);
     }
   }
 
@@ -149,7 +200,9 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
       for (int m = P / 2; m >= 1; m >>= 1) part += shfl_xor(part, m);
       const uint32_t row = (g0 + waves * u) * R + sub;
       if (ll == 0 && g0 + waves * u < n_groups && row < a.n_rows) {
-        if (a.o != nullptr) a.o[(size_t)tok * a.n_rows + row] = part;
+        const size_t oi = (size_t)tok * a.n_rows + row;
+        if (a.res != nullptr) part = a.res[oi] + part;
+        if (a.o != nullptr) a.o[oi] = part;
         if (argmax_better(part, row, bv, bi)) {
           bv = part;
           bi = row;
@@ -168,7 +221,9 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
   const uint32_t nb = a.n_cols / 32;
   const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
   const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
-  const float* xt = a.x + (size_t)tok * a.n_cols;
+  const size_t tok_off = (size_t)tok * a.n_cols;
+  const float* xt = a.x + tok_off;
+  const float scale = q8_norm_scale(a, xt);
   float bv = kArgmaxNoVal;
   uint32_t bi = kArgmaxNoIdx;
   for (uint32_t row = wave; row < a.n_rows; row += waves) {
@@ -176,21 +231,16 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
     for (uint32_t b = lane; b < nb; b += kQ8Lanes) {
       const uint4* src = reinterpret_cast<const uint4*>(a.qs + (size_t)row * a.n_cols + 32 * (size_t)b);
       float xb[32];
-      const float4* xs = reinterpret_cast<const float4*>(xt + 32 * (size_t)b);
 #pragma unroll
-      for (int i = 0; i < 8; i++) {
-        const float4 v = xs[i];
-        xb[4 * i + 0] = v.x;
-        xb[4 * i + 1] = v.y;
-        xb[4 * i + 2] = v.z;
-        xb[4 * i + 3] = v.w;
-      }
+      for (int i = 0; i < 32; i++) xb[i] = q8_xin(a, xt, tok_off, 32 * b + i, scale);
       part = q8_block(part, q8_scale(a.scales[(size_t)row * nb + b]), src[0], src[1], xb);
     }
 #pragma unroll
     for (int m = 32; m >= 1; m >>= 1) part += shfl_xor(part, m);
     if (lane == 0) {
-      if (a.o != nullptr) a.o[(size_t)tok * a.n_rows + row] = part;
+      const size_t oi = (size_t)tok * a.n_rows + row;
+      if (a.res != nullptr) part = a.res[oi] + part;
+      if (a.o != nullptr) a.o[oi] = part;
       if (argmax_better(part, row, bv, bi)) {
         bv = part;
         bi = row;
@@ -203,13 +253,13 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
 // Workgroups: one resident wave of them (every CU filled to its occupancy
 // limit, so no workgroup waits for another to finish), never more than there
 // are row groups.
-template <int P, int NB>
+template <int P, int NB, bool FUSE>
 static uint32_t q8_grid_x(uint32_t n_groups) {
   static int per_cu = 0;
   if (per_cu == 0) {
     int n = 0;
     if (FLK_Q8_WG_PER_CU > 0 ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, q8_matvec_kernel<P, NB>, kQ8Threads, 0) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, q8_matvec_kernel<P, NB, FUSE>, kQ8Threads, 0) !=
             hipSuccess ||
         n < 1)
       n = FLK_Q8_WG_PER_CU > 0 ? FLK_Q8_WG_PER_CU : 2;
@@ -232,8 +282,15 @@ static uint32_t q8_grid_x(uint32_t n_groups) {
 template <int P, int NB>
 static uint32_t launch_q8(const Q8Args& a, hipStream_t st) {
   const uint32_t groups = (a.n_rows + (kWave / P) - 1) / (kWave / P);
-  const uint32_t gx = q8_grid_x<P, NB>(groups);
-  hipLaunchKernelGGL((q8_matvec_kernel<P, NB>), dim3(gx, a.n_tokens), dim3(kQ8Threads), 0, st, a);
+  if (a.norm_gain != nullptr || a.up != nullptr) {
+    const uint32_t gx = q8_grid_x<P, NB, true>(groups);
+    hipLaunchKernelGGL((q8_matvec_kernel<P, NB, true>), dim3(gx, a.n_tokens), dim3(kQ8Threads), 0,
+                       st, a);
+    return gx;
+  }
+  const uint32_t gx = q8_grid_x<P, NB, false>(groups);
+  hipLaunchKernelGGL((q8_matvec_kernel<P, NB, false>), dim3(gx, a.n_tokens), dim3(kQ8Threads), 0,
+                     st, a);
   return gx;
 }
 
@@ -252,8 +309,15 @@ uint32_t q8_max_workgroups(uint32_t n_rows, uint32_t n_cols) {
 hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const float* x, float* o,
                             uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
                             hipStream_t st, float* best_val, uint32_t* best_idx,
-                            uint32_t* n_workgroups) {
-  Q8Args a{qs, scales, x, o, n_rows, n_cols, n_tokens, best_val, best_idx};
+                            uint32_t* n_workgroups, const Q8Fuse* fuse) {
+  Q8Args a{qs, scales, x, o, n_rows, n_cols, n_tokens, best_val, best_idx,
+           nullptr, 0.f, nullptr, nullptr};
+  if (fuse != nullptr) {
+    a.norm_gain = fuse->norm_gain;
+    a.norm_eps = fuse->norm_eps;
+    a.up = fuse->up;
+    a.res = fuse->res;
+  }
   const uint32_t nb = n_cols / 32;
   uint32_t gx;
   if (nb > (uint32_t)kQ8Lanes * kQ8MaxRegBlocks) {

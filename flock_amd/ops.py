@@ -239,6 +239,24 @@ def q8_matvec(w, x, o, n_tokens: int = 1, qs=None, scales=None, n_rows: int | No
           "flk_q8_matvec")
 
 
+def q8_matvec_ex(w: "Q8Matrix", x, o, n_tokens: int = 1, norm_gain=None, eps: float = 0.0,
+                 up=None, res=None) -> None:
+    """flk_q8_matvec_ex: o = [res +] W f(x), f = rmsnorm (norm_gain) or swiglu(., up)."""
+    check(lib().flk_q8_matvec_ex(ptr(w.qs), ptr(w.scales), ptr(x), ptr(o), w.rows, w.cols,
+                                 n_tokens, ptr(norm_gain), eps, ptr(up), ptr(res)),
+          "flk_q8_matvec_ex")
+
+
+def swiglu(gate, up, o, n: int) -> None:
+    """elementwise.wgsl swiglu: o = silu(gate) * up."""
+    check(lib().flk_swiglu(ptr(gate), ptr(up), ptr(o), n), "flk_swiglu")
+
+
+def add(a, b, o, n: int) -> None:
+    """elementwise.wgsl add: o = a + b."""
+    check(lib().flk_add(ptr(a), ptr(b), ptr(o), n), "flk_add")
+
+
 # ---------------------------------------------------------------- the head
 def argmax_ws_bytes(n: int) -> int:
     return int(lib().flk_argmax_ws_bytes(n))

@@ -32,6 +32,30 @@ extern "C" {
 int32_t flk_q8_matvec(const int8_t* qs, const uint16_t* scales, const float* x, float* o,
                       uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens);
 
+/* flk_q8_matvec with the layer's neighbouring elementwise ops folded in
+ * (Layer.encode, layer.ts:590-649, does them as separate dispatches):
+ *   norm_gain != NULL: x is first RMS-normalised per token over n_cols with
+ *     that gain and eps (rmsnorm.wgsl, one vector per token) -- the
+ *     attn_norm / ffn_norm before the q/k/v and gate/up projections;
+ *   up != NULL: x is first replaced by swiglu(x, up) elementwise
+ *     (elementwise.wgsl swiglu; up is [n_tokens][n_cols]) -- before ffn_down;
+ *   res != NULL: o = res + W x (elementwise.wgsl add; res is
+ *     [n_tokens][n_rows], may equal o) -- the residual adds.
+ * norm_gain and up are exclusive. Results are bit-identical to the separate
+ * ops (rmsnormRef / swigluRef / addRef, then cpuMatmulQ8F32 coop(64)) except
+ * that swiglu's exp is evaluated in f64 and rounded once, as the CPU
+ * reference does (the WGSL kernel uses f32 exp). */
+int32_t flk_q8_matvec_ex(const int8_t* qs, const uint16_t* scales, const float* x, float* o,
+                         uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
+                         const float* norm_gain, float norm_eps, const float* up,
+                         const float* res);
+
+/* elementwise.wgsl (kernels/elementwise.wgsl:24-37) on n floats:
+ * swiglu o = silu(gate) * up = fr(fr(g / fr(1 + fr(exp(-g)))) * up) (exp in
+ * f64, rounded once, as swigluRef); add o = a + b. o may alias an input. */
+int32_t flk_swiglu(const float* gate, const float* up, float* o, uint32_t n);
+int32_t flk_add(const float* a, const float* b, float* o, uint32_t n);
+
 /* splitQ8 (kernels/lib.ts:141-156) on the host: packed is n_rows * n_cols / 32
  * blocks of 34 bytes (f16 scale, little-endian, then 32 int8); writes qs
  * [n_rows * n_cols] and scales [n_rows * n_cols / 32]. HOST pointers. */

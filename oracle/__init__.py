@@ -75,6 +75,8 @@ def lib() -> ctypes.CDLL:
             "flko_split_q8": (None, [_u8p, i, i, _u8p, _u8p]),
             "flko_q8_matvec": (None, [_u8p, _f32p, i, i, i, i, _f32p]),
             "flko_argmax_wgsl": (None, [_f32p, i64, _f32p, ctypes.POINTER(ctypes.c_uint32)]),
+            "flko_swiglu": (None, [_f32p, _f32p, _f32p, i64]),
+            "flko_add": (None, [_f32p, _f32p, _f32p, i64]),
         }
         for name, (res, args) in sig.items():
             fn = getattr(L, name)
@@ -301,3 +303,64 @@ def lm_head(x, gain, eps: float, packed, vocab: int, hidden: int):
     logits = q8_matvec(packed, normed, vocab, hidden, 64, fused=True)
     v, i = argmax_wgsl(logits)
     return normed, logits, v, i
+
+
+def swiglu(gate, up) -> np.ndarray:
+    """swigluRef, kernels/ops_ref.ts:103-110."""
+    gate, up = _f32(gate).ravel(), _f32(up).ravel()
+    assert gate.size == up.size
+    o = np.empty(gate.size, np.float32)
+    lib().flko_swiglu(_p(gate), _p(up), _p(o), gate.size)
+    return o
+
+
+def add(a, b) -> np.ndarray:
+    """addRef, kernels/ops_ref.ts:113-117."""
+    a, b = _f32(a).ravel(), _f32(b).ravel()
+    assert a.size == b.size
+    o = np.empty(a.size, np.float32)
+    lib().flko_add(_p(a), _p(b), _p(o), a.size)
+    return o
+
+
+def layer_forward(hidden, w: dict, cfg: dict, kcache: np.ndarray, vcache: np.ndarray, pos: int,
+                  fused: bool = False) -> np.ndarray:
+    """layerForwardRef (kernels/layer_ref.ts:32-82): one decode step of a whole
+    Qwen3 layer, composed of the restated ops. ``w`` maps the reference's
+    tensor names to 34-byte Q8_0 bytes (projections) or f32 gains; the cache
+    rows ``pos`` are written in place. Returns the layer output."""
+    H, Hkv, d = cfg["nHeads"], cfg["nKvHeads"], cfg["headDim"]
+    hid, ffn, eps = cfg["hidden"], cfg["ffn"], cfg["eps"]
+    mv = lambda name, x, rows, cols: q8_matvec(w[name], x, rows, cols, 64, fused)  # noqa: E731
+    nh = rmsnorm(hidden, w["attn_norm.weight"], hid, 1, eps)
+    q = mv("attn_q.weight", nh, H * d, hid)
+    k = mv("attn_k.weight", nh, Hkv * d, hid)
+    v = mv("attn_v.weight", nh, Hkv * d, hid)
+    _, attn_o = layer_attn_decode(q, k, v, w["attn_q_norm.weight"], w["attn_k_norm.weight"],
+                                  rope_inv_freq(d, cfg.get("ropeBase", QWEN3_ROPE_BASE)), kcache,
+                                  vcache, pos, H, Hkv, d, eps, cfg.get("ropePairing", "neox"))
+    h = add(hidden, mv("attn_output.weight", attn_o, hid, H * d))
+    nh2 = rmsnorm(h, w["ffn_norm.weight"], hid, 1, eps)
+    act = swiglu(mv("ffn_gate.weight", nh2, ffn, hid), mv("ffn_up.weight", nh2, ffn, hid))
+    return add(h, mv("ffn_down.weight", act, hid, ffn))
+
+
+def layer_prefill(hidden, n: int, w: dict, cfg: dict, kcache: np.ndarray, vcache: np.ndarray,
+                  pos0: int, fused: bool = False) -> np.ndarray:
+    """layerPrefillRef (kernels/layer_ref.ts:84-177): n tokens at positions
+    pos0 .. pos0+n-1; the batched matvec is the per-token one (layer_ref.ts:
+    112-128). Cache rows are written in place; returns [n][hidden]."""
+    H, Hkv, d = cfg["nHeads"], cfg["nKvHeads"], cfg["headDim"]
+    hid, ffn, eps = cfg["hidden"], cfg["ffn"], cfg["eps"]
+    mv = lambda name, x, rows, cols: q8_matvec(w[name], x, rows, cols, 64, fused)  # noqa: E731
+    nh = rmsnorm(hidden, w["attn_norm.weight"], hid, n, eps)
+    q = mv("attn_q.weight", nh, H * d, hid)
+    k = mv("attn_k.weight", nh, Hkv * d, hid)
+    v = mv("attn_v.weight", nh, Hkv * d, hid)
+    _, attn_o = layer_attn_prefill(q, k, v, w["attn_q_norm.weight"], w["attn_k_norm.weight"],
+                                   rope_inv_freq(d, cfg.get("ropeBase", QWEN3_ROPE_BASE)), kcache,
+                                   vcache, n, pos0, H, Hkv, d, eps, cfg.get("ropePairing", "neox"))
+    h = add(hidden, mv("attn_output.weight", attn_o, hid, H * d))
+    nh2 = rmsnorm(h, w["ffn_norm.weight"], hid, n, eps)
+    act = swiglu(mv("ffn_gate.weight", nh2, ffn, hid), mv("ffn_up.weight", nh2, ffn, hid))
+    return add(h, mv("ffn_down.weight", act, hid, ffn))

@@ -24,6 +24,7 @@
  *                        pairwise treeSum (lib.ts:312-318).
  *   flko_argmax_wgsl     argmax.wgsl's two-pass contract (lowest index among
  *                        equal maxima, NaN never chosen, empty sentinel).
+ *   flko_swiglu, flko_add  swigluRef / addRef (kernels/ops_ref.ts:103-117).
  *
  * `fused` selects the FMA model: 0 = the reference's fma32 (f64 a*b + c,
  * then rounded to f32: two roundings), 1 = fmaf (one rounding, what the GPU's
@@ -39,7 +40,9 @@
  * exact sum, so a wrong index or operand fails), against an f64 sum within
  * the f32 error bound, and coop against serial on integer inputs;
  * argmax_wgsl against numpy's argmax / nanargmax (lowest index of the
- * maximum) and hand-derived sentinel cases.
+ * maximum) and hand-derived sentinel cases; swiglu against numpy f64
+ * silu(g) * up within 2 ulp and on exact cases (g = 0, up = 0); add against
+ * numpy f32 addition.
  */
 #include <math.h>
 #include <stdint.h>
@@ -188,4 +191,19 @@ void flko_argmax_wgsl(const float* x, int64_t n, float* oval, uint32_t* oidx) {
     }
   *oval = bv;
   *oidx = bi;
+}
+
+/* swigluRef (kernels/ops_ref.ts:103-110): fr(fr(g / fr(1 + fr(exp(-g)))) * up). */
+void flko_swiglu(const float* gate, const float* up, float* o, int64_t n) {
+  for (int64_t i = 0; i < n; i++) {
+    const float g = gate[i];
+    const float e = fr64(exp(-(double)g));
+    const float den = fr64(1.0 + (double)e);
+    o[i] = fr64((double)fr64((double)g / (double)den) * (double)up[i]);
+  }
+}
+
+/* addRef (kernels/ops_ref.ts:113-117). */
+void flko_add(const float* a, const float* b, float* o, int64_t n) {
+  for (int64_t i = 0; i < n; i++) o[i] = fr64((double)a[i] + (double)b[i]);
 }

@@ -226,6 +226,34 @@ def test_decode_layer_fused_matches_oracle(rng):
     assert meets_bar(m), fmt(m)
 
 
+@pytest.mark.parametrize("pos", [0, 1, 5, 700, 5000])
+def test_decode_layer_ignores_the_row_being_appended(rng, pos):
+    # The row at pos is written by one workgroup of the same launch; before
+    # that it may hold anything (here NaN). Workgroups whose last block runs
+    # past the end re-read that row; its contents must never reach the output.
+    H, Hkv, d = 16, 8, 128
+    maxk = pos + 1
+    kc0, vc0 = randn(rng, maxk * Hkv * d), randn(rng, maxk * Hkv * d)
+    row = Hkv * d
+    kc0[pos * row:] = np.nan
+    vc0[pos * row:] = np.nan
+    q, k, v = randn(rng, H * d), randn(rng, Hkv * d), randn(rng, Hkv * d)
+    gq = rng.normal(1, 0.1, d).astype(np.float32)
+    gk = rng.normal(1, 0.1, d).astype(np.float32)
+    inv = ops.rope_inv_freq(d, 1e6)
+    kc, vc = dev(kc0), dev(vc0)
+    qn, o = empty(H * d), empty(H * d)
+    ws = ops.Workspace(H, Hkv, d, maxk)
+    ops.decode_layer(dev(q), dev(k), dev(v), dev(gq), dev(gk), dev(inv), EPS, "neox", qn, kc, vc,
+                     o, pos, H, Hkv, d, maxk, ws)
+    got_o = get(o, H * d)
+    kco, vco = kc0.copy(), vc0.copy()
+    want_qn, want_o = oracle.layer_attn_decode(q, k, v, gq, gk, inv, kco, vco, pos, H, Hkv, d)
+    assert not np.isnan(got_o).any()
+    m = metrics(got_o, want_o, cf.attention(want_qn, kco, vco, H, Hkv, d, 1, pos))
+    assert meets_bar(m), fmt(m)
+
+
 # ------------------------------------------------------------------ prefill --
 def _prefill(q, k, v, H, Hkv, d, nq, pos0):
     ws = ops.Workspace(H, Hkv, d, pos0 + nq, nq)

@@ -209,3 +209,110 @@ def test_argmax_wgsl_nan_and_sentinel():
     assert i == 0xFFFFFFFF and v == -F32_MAX
     # -FLT_MAX itself wins (equal to the start value, lower index).
     assert oracle.argmax_wgsl(np.array([-np.inf, -F32_MAX], np.float32))[1] == 1
+
+
+# ---------------------------------------------------------------- swiglu / add
+def test_swiglu_against_f64_and_exact_cases():
+    rng = np.random.default_rng(21)
+    g = (rng.standard_normal(100000) * 4).astype(np.float32)
+    u = rng.standard_normal(100000).astype(np.float32)
+    got = oracle.swiglu(g, u).astype(np.float64)
+    g64 = g.astype(np.float64)
+    want = g64 / (1 + np.exp(-g64)) * u.astype(np.float64)
+    ulp = np.spacing(np.abs(want).astype(np.float32)).astype(np.float64)
+    # Four f32 roundings (exp, 1 + e, the quotient, the product), each within
+    # half an ulp of its own value: at most 4 ulp of the result.
+    assert np.all(np.abs(got - want) <= 4 * ulp)
+    z = oracle.swiglu(np.zeros(4, np.float32), np.ones(4, np.float32))
+    assert np.array_equal(z, np.zeros(4, np.float32))
+    assert np.array_equal(oracle.swiglu(g[:8], np.zeros(8, np.float32)), np.zeros(8, np.float32))
+    # Large positive g: silu(g) == g exactly once exp(-g) underflows below ulp(1).
+    assert oracle.swiglu(np.float32([100.0]), np.float32([3.0]))[0] == np.float32(300.0)
+
+
+def test_add_is_f32_addition():
+    rng = np.random.default_rng(22)
+    a = rng.standard_normal(5000).astype(np.float32)
+    b = rng.standard_normal(5000).astype(np.float32)
+    assert np.array_equal(oracle.add(a, b), a + b)
+
+
+# ---------------------------------------------------------------- whole layer
+def tiny_layer(rng, hid=128, ffn=256, H=4, Hkv=2, d=64):
+    cfg = dict(nHeads=H, nKvHeads=Hkv, headDim=d, hidden=hid, ffn=ffn, eps=oracle.QWEN3_EPS)
+    shapes = {"attn_q.weight": (H * d, hid), "attn_k.weight": (Hkv * d, hid),
+              "attn_v.weight": (Hkv * d, hid), "attn_output.weight": (hid, H * d),
+              "ffn_gate.weight": (ffn, hid), "ffn_up.weight": (ffn, hid),
+              "ffn_down.weight": (hid, ffn)}
+    w = {n: oracle.quant_matrix_q8((rng.standard_normal(r * c) * 0.05).astype(np.float32), r, c)
+         for n, (r, c) in shapes.items()}
+    for n, sz in (("attn_norm.weight", hid), ("ffn_norm.weight", hid),
+                  ("attn_q_norm.weight", d), ("attn_k_norm.weight", d)):
+        w[n] = rng.normal(1, 0.1, sz).astype(np.float32)
+    return cfg, w, shapes
+
+
+def dequant(packed, rows, cols):
+    qs, sc = oracle.split_q8(packed, rows, cols)
+    s = np.array([oracle.half_to_f32(int(h)) for h in sc]).reshape(rows, cols // 32, 1)
+    return (qs.astype(np.float64).reshape(rows, cols // 32, 32) * s).reshape(rows, cols)
+
+
+def layer_f64(hidden, n, w, shapes, cfg, kc, vc, pos0):
+    """The layer's mathematics in float64 (dequantized weights), for wiring."""
+    from oracle import closed_form as cf
+    H, Hkv, d, hid, eps = cfg["nHeads"], cfg["nKvHeads"], cfg["headDim"], cfg["hidden"], cfg["eps"]
+    W = {k: dequant(w[k], *shapes[k]) for k in shapes}
+    x = hidden.reshape(n, hid).astype(np.float64)
+    nh = cf.rmsnorm(x.ravel(), w["attn_norm.weight"], hid, n, eps).reshape(n, hid)
+    q = nh @ W["attn_q.weight"].T
+    k = nh @ W["attn_k.weight"].T
+    v = nh @ W["attn_v.weight"].T
+    inv = cf.inv_freq(d, 1e6)
+    q = cf.rope(cf.rmsnorm(q.ravel(), w["attn_q_norm.weight"], d, n * H, eps), n, H, d, pos0, inv)
+    k = cf.rope(cf.rmsnorm(k.ravel(), w["attn_k_norm.weight"], d, n * Hkv, eps), n, Hkv, d, pos0, inv)
+    row = Hkv * d
+    kc[pos0 * row:(pos0 + n) * row] = k
+    vc[pos0 * row:(pos0 + n) * row] = v.ravel()
+    a = cf.attention(q, kc, vc, H, Hkv, d, n, pos0).reshape(n, H * d)
+    h = x + a @ W["attn_output.weight"].T
+    nh2 = cf.rmsnorm(h.ravel(), w["ffn_norm.weight"], hid, n, eps).reshape(n, -1)
+    g, u = nh2 @ W["ffn_gate.weight"].T, nh2 @ W["ffn_up.weight"].T
+    return (h + (g / (1 + np.exp(-g)) * u) @ W["ffn_down.weight"].T).ravel()
+
+
+@pytest.mark.parametrize("n,pos0", [(1, 0), (1, 9), (5, 0), (6, 11)])
+def test_layer_composition_against_f64(n, pos0):
+    rng = np.random.default_rng(31 + n + pos0)
+    cfg, w, shapes = tiny_layer(rng)
+    hid, row = cfg["hidden"], cfg["nKvHeads"] * cfg["headDim"]
+    maxk = pos0 + n
+    kc = np.zeros(maxk * row, np.float32)
+    vc = np.zeros(maxk * row, np.float32)
+    kc[:pos0 * row] = rng.standard_normal(pos0 * row)
+    vc[:pos0 * row] = rng.standard_normal(pos0 * row)
+    kc64, vc64 = kc.astype(np.float64), vc.astype(np.float64)
+    hidden = rng.standard_normal(n * hid).astype(np.float32)
+    if n == 1:
+        got = oracle.layer_forward(hidden, w, cfg, kc, vc, pos0)
+    else:
+        got = oracle.layer_prefill(hidden, n, w, cfg, kc, vc, pos0)
+    want = layer_f64(hidden, n, w, shapes, cfg, kc64, vc64, pos0)
+    assert np.max(np.abs(got - want)) < 1e-4 * max(1.0, np.max(np.abs(want)))
+    assert np.max(np.abs(kc - kc64)) < 1e-5 and np.max(np.abs(vc - vc64)) < 1e-6
+
+
+def test_layer_prefill_rows_equal_decode_steps():
+    # layerPrefillRef over n tokens == n layerForwardRef steps (same cache, same
+    # outputs), because every op is per token or causal (test_prefill.ts:119-132).
+    rng = np.random.default_rng(40)
+    cfg, w, _ = tiny_layer(rng)
+    n, hid, row = 4, cfg["hidden"], cfg["nKvHeads"] * cfg["headDim"]
+    hidden = rng.standard_normal(n * hid).astype(np.float32)
+    kc1, vc1 = np.zeros(n * row, np.float32), np.zeros(n * row, np.float32)
+    pre = oracle.layer_prefill(hidden, n, w, cfg, kc1, vc1, 0)
+    kc2, vc2 = np.zeros(n * row, np.float32), np.zeros(n * row, np.float32)
+    steps = np.concatenate([oracle.layer_forward(hidden[i * hid:(i + 1) * hid], w, cfg, kc2, vc2, i)
+                            for i in range(n)])
+    assert np.array_equal(kc1, kc2) and np.array_equal(vc1, vc2)
+    assert np.max(np.abs(pre - steps)) < 1e-5
