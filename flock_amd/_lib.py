@@ -64,6 +64,11 @@ SIGNATURES: dict[str, tuple] = {
     "flk_q8_matvec_ex": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32, _p, _f32, _p, _p]),
     "flk_swiglu": (_i32, [_p, _p, _p, _u32]),
     "flk_add": (_i32, [_p, _p, _p, _u32]),
+    # include/flock_wire.h
+    "flk_f32_to_f16": (_i32, [_p, _p, _u64]),
+    "flk_f16_to_f32": (_i32, [_p, _p, _u64]),
+    "flk_wire_header_pack": (_i32, [_u32, _u32, _u32, _u32, _p]),
+    "flk_wire_header_unpack": (_i32, [_p, _u64, _p, _p, _p, _p, _p]),
     "flk_argmax_ws_bytes": (_u64, [_u32]),
     "flk_argmax": (_i32, [_p, _u32, _p, _p, _p, _u64]),
     "flk_lm_head_ws_bytes": (_u64, [_u32, _u32]),

@@ -487,3 +487,58 @@ int32_t flk_q8_split(const uint8_t* packed, uint32_t n_rows, uint32_t n_cols, in
     }
   return FLK_OK;
 }
+
+// ------------------------------------------------------------------ wire ---
+int32_t flk_f32_to_f16(const float* in, uint16_t* out, uint64_t n) {
+  FLK_NONNULL(in);
+  FLK_NONNULL(out);
+  if (n == 0) return FLK_OK;
+  return hip_status(launch_wire(0, in, out, n, g_stream), "flk_f32_to_f16");
+}
+
+int32_t flk_f16_to_f32(const uint16_t* in, float* out, uint64_t n) {
+  FLK_NONNULL(in);
+  FLK_NONNULL(out);
+  if (n == 0) return FLK_OK;
+  return hip_status(launch_wire(1, in, out, n, g_stream), "flk_f16_to_f32");
+}
+
+static void put_u32(uint8_t* p, uint32_t v) {
+  p[0] = (uint8_t)v;
+  p[1] = (uint8_t)(v >> 8);
+  p[2] = (uint8_t)(v >> 16);
+  p[3] = (uint8_t)(v >> 24);
+}
+
+static uint32_t get_u32(const uint8_t* p) {
+  return (uint32_t)p[0] | ((uint32_t)p[1] << 8) | ((uint32_t)p[2] << 16) | ((uint32_t)p[3] << 24);
+}
+
+// pack (wire.mjs:66-78): magic, seq, hidden, offset, flags, little-endian.
+int32_t flk_wire_header_pack(uint32_t seq, uint32_t hidden, uint32_t offset, uint32_t flags,
+                             void* out20) {
+  FLK_NONNULL(out20);
+  uint8_t* p = static_cast<uint8_t*>(out20);
+  put_u32(p, FLK_WIRE_MAGIC);
+  put_u32(p + 4, seq);
+  put_u32(p + 8, hidden);
+  put_u32(p + 12, offset);
+  put_u32(p + 16, flags & (FLK_WIRE_RESET | FLK_WIRE_REPLAY));
+  return FLK_OK;
+}
+
+// unpack's header (wire.mjs:80-88).
+int32_t flk_wire_header_unpack(const void* frame, uint64_t frame_bytes, uint32_t* seq,
+                               uint32_t* hidden, uint32_t* offset, uint32_t* flags,
+                               uint64_t* n_values) {
+  FLK_NONNULL(frame);
+  const uint8_t* p = static_cast<const uint8_t*>(frame);
+  if (frame_bytes < FLK_WIRE_HEADER_BYTES || get_u32(p) != FLK_WIRE_MAGIC)
+    return fail(FLK_ERR_ARG, "not a flock frame");
+  if (seq) *seq = get_u32(p + 4);
+  if (hidden) *hidden = get_u32(p + 8);
+  if (offset) *offset = get_u32(p + 12);
+  if (flags) *flags = get_u32(p + 16);
+  if (n_values) *n_values = (frame_bytes - FLK_WIRE_HEADER_BYTES) / 2;
+  return FLK_OK;
+}

@@ -6,6 +6,7 @@
 
 #include "../../include/flock_attn.h"
 #include "../../include/flock_q8.h"
+#include "../../include/flock_wire.h"
 #include "trig.hpp"
 
 namespace flk {
@@ -253,6 +254,9 @@ uint32_t q8_max_workgroups(uint32_t n_rows, uint32_t n_cols);
 // op 0: swiglu(a, b); op 1: a + b (elementwise.wgsl).
 hipError_t launch_elementwise(int op, const float* a, const float* b, float* o, uint32_t n,
                               hipStream_t st);
+
+// dir 0: f32 -> f16 (wire pack), 1: f16 -> f32 (wire unpack).
+hipError_t launch_wire(int dir, const void* in, void* out, uint64_t n, hipStream_t st);
 
 // ------------------------------------------------------------------- head ----
 uint64_t argmax_ws_bytes(uint32_t n);

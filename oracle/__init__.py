@@ -76,6 +76,7 @@ def lib() -> ctypes.CDLL:
             "flko_q8_matvec": (None, [_u8p, _f32p, i, i, i, i, _f32p]),
             "flko_argmax_wgsl": (None, [_f32p, i64, _f32p, ctypes.POINTER(ctypes.c_uint32)]),
             "flko_swiglu": (None, [_f32p, _f32p, _f32p, i64]),
+            "flko_f16_to_f32_wire": (d, [ctypes.c_uint16]),
             "flko_add": (None, [_f32p, _f32p, _f32p, i64]),
         }
         for name, (res, args) in sig.items():
@@ -364,3 +365,34 @@ def layer_prefill(hidden, n: int, w: dict, cfg: dict, kcache: np.ndarray, vcache
     nh2 = rmsnorm(h, w["ffn_norm.weight"], hid, n, eps)
     act = swiglu(mv("ffn_gate.weight", nh2, ffn, hid), mv("ffn_up.weight", nh2, ffn, hid))
     return add(h, mv("ffn_down.weight", act, hid, ffn))
+
+
+# ---------------------------------------------------------------- FLK1 frames
+WIRE_MAGIC = 0x314B4C46  # "FLK1" little-endian (web/js/wire.mjs:25)
+
+
+def f16_to_f32_wire(h: int) -> float:
+    """f16to32, web/js/wire.mjs:55-61 (inf and NaN kept)."""
+    return float(lib().flko_f16_to_f32_wire(int(h) & 0xFFFF))
+
+
+def wire_pack(floats, seq: int, hidden: int, offset: int = 0, reset: bool = False,
+              replay: bool = False) -> bytes:
+    """pack, web/js/wire.mjs:66-78."""
+    import struct
+    a = _f32(floats).ravel()
+    head = struct.pack("<5I", WIRE_MAGIC, seq, hidden, offset, (1 if reset else 0) | (2 if replay else 0))
+    return head + f32_to_f16_array(a).astype("<u2").tobytes()
+
+
+def wire_unpack(buf: bytes):
+    """unpack, web/js/wire.mjs:80-94: (data f32, meta dict)."""
+    import struct
+    if len(buf) < 20 or struct.unpack_from("<I", buf, 0)[0] != WIRE_MAGIC:
+        raise ValueError("not a flock frame")
+    _, seq, hidden, offset, flags = struct.unpack_from("<5I", buf, 0)
+    n = (len(buf) - 20) // 2
+    hs = np.frombuffer(buf, "<u2", n, 20)
+    data = np.array([f16_to_f32_wire(int(h)) for h in hs], np.float32)
+    return data, dict(seq=seq, hidden=hidden, offset=offset, reset=bool(flags & 1),
+                      replay=bool(flags & 2))

@@ -25,6 +25,7 @@
  *   flko_argmax_wgsl     argmax.wgsl's two-pass contract (lowest index among
  *                        equal maxima, NaN never chosen, empty sentinel).
  *   flko_swiglu, flko_add  swigluRef / addRef (kernels/ops_ref.ts:103-117).
+ *   flko_f16_to_f32_wire f16to32 (web/js/wire.mjs:55-61), the frame decoder.
  *
  * `fused` selects the FMA model: 0 = the reference's fma32 (f64 a*b + c,
  * then rounded to f32: two roundings), 1 = fmaf (one rounding, what the GPU's
@@ -206,4 +207,13 @@ void flko_swiglu(const float* gate, const float* up, float* o, int64_t n) {
 /* addRef (kernels/ops_ref.ts:113-117). */
 void flko_add(const float* a, const float* b, float* o, int64_t n) {
   for (int64_t i = 0; i < n; i++) o[i] = fr64((double)a[i] + (double)b[i]);
+}
+
+/* f16to32 (web/js/wire.mjs:55-61): exponent 31 is inf or NaN (not clamped). */
+double flko_f16_to_f32_wire(uint16_t h) {
+  const double s = (h & 0x8000u) ? -1.0 : 1.0;
+  const int e = (h >> 10) & 0x1f, m = h & 0x3ff;
+  if (e == 0) return s * m * ldexp(1.0, -24);
+  if (e == 31) return m ? NAN : s * INFINITY;
+  return s * (1.0 + m / 1024.0) * ldexp(1.0, e - 15);
 }
