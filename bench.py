@@ -26,6 +26,10 @@ of the hot path over one batch of synthetic, HBM-resident input:
              151936 x 1024 LM head, one token (flk_q8_matvec). GB/s.
   q8proj     The seven Q8_0 projections of all 28 layers for one decode
              token (196 flk_q8_matvec calls). GB/s.
+  token32k   One greedy decode token through the whole model: 28 decoder
+             layers (DecoderLayer: fused projections + attention over 32769
+             keys) + output norm + LM head + argmax. GB/s and tokens/s.
+  token512   The same at 513 keys (launch-bound).
 
 The default run also measures prefill2k (the metric's second half) and reports
 it under "prefill", and the LM-head projection under "q8_lm_head". Inputs are N(0, 1) from a seeded generator (gains
@@ -457,8 +461,89 @@ class Q8Proj(Workload):
                     r * c * 34 // 32 for r, c in self.shapes)}
 
 
+class Token(Workload):
+    """One greedy decode token through all 28 Qwen3-0.6B layers and the head:
+    per layer the five DecoderLayer calls (fused projections + the attention
+    slice), then flk_lm_head (output norm, tied 151936 x 1024 projection,
+    argmax). Random Q8_0 weights, zeroed caches at position n_keys - 1."""
+
+    unit = "GB/s"
+    kernel = ("DecoderLayer.encode x 28 + flk_lm_head (q8_matvec_kernel, decode_split/merge, "
+              "argmax_final_kernel)")
+    n_keys = 32769
+    layers = 28
+
+    def __init__(self, torch, ops):
+        from flock_amd.decoder import DecoderConfig, DecoderLayer
+        self.torch, self.ops = torch, ops
+        rng = np.random.default_rng(12)
+        cfg = DecoderConfig(maxKeys=self.n_keys, maxPrefill=1)
+        log(f"[{self.name}] building {self.layers} layers (random Q8_0 weights)")
+
+        def packed(rows, cols):
+            blocks = np.empty((rows * cols // 32, 34), np.uint8)
+            blocks[:, :2] = (rng.random(blocks.shape[0]) * 8e-4 + 1e-5).astype(
+                np.float16).view(np.uint8).reshape(-1, 2)
+            blocks[:, 2:] = rng.integers(0, 256, (blocks.shape[0], 32), dtype=np.uint8)
+            return blocks.ravel()
+
+        self.L = []
+        for _ in range(self.layers):
+            w = {n: packed(r, c) for n, (r, c) in cfg.shapes().items()}
+            for n, sz in (("attn_norm.weight", cfg.hidden), ("ffn_norm.weight", cfg.hidden),
+                          ("attn_q_norm.weight", cfg.headDim), ("attn_k_norm.weight", cfg.headDim)):
+                w[n] = (1 + 0.1 * rng.standard_normal(sz)).astype(np.float32)
+            layer = DecoderLayer.create(cfg, w)
+            layer.buf["kcache"].zero()
+            layer.buf["vcache"].zero()
+            self.L.append(layer)
+        self.vocab, self.hid = 151936, cfg.hidden
+        self.head = ops.Q8Matrix.from_packed(packed(self.vocab, self.hid), self.vocab, self.hid)
+        self.gout = ops.DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(self.hid)).astype(np.float32))
+        self.normed = ops.DeviceBuffer(self.hid * 4)
+        self.tok_v, self.tok_i = ops.DeviceBuffer(4), ops.DeviceBuffer(4)
+        self.hws = ops.DeviceBuffer(ops.lm_head_ws_bytes(self.vocab, self.hid))
+        self.x = ops.DeviceBuffer.from_array(rng.standard_normal(self.hid).astype(np.float32))
+        layer_w = sum(r * c * 34 // 32 for r, c in cfg.shapes().values())
+        kv = 2 * self.n_keys * cfg.nKvHeads * cfg.headDim * 4
+        self.work_per_call = self.layers * (layer_w + kv) + self.vocab * self.hid * 34 // 32
+        self.work_per_step = self.work_per_call
+        self.calls_per_step = 1
+
+    def call(self, l=0):
+        src = self.x
+        for layer in self.L:
+            layer.nKeys = self.n_keys - 1
+            layer.encode(src=src)
+            src = layer.outputBuffer()
+        self.ops.lm_head(src, self.gout, EPS, self.head, self.normed, None, self.tok_v, self.tok_i,
+                         self.hws)
+
+    def step(self):
+        self.call()
+
+    def extra(self, ms):
+        return {"tokens_per_s": round(1e3 / ms, 2), "ms_per_token": round(ms, 4)}
+
+    def config(self):
+        return {"workload": f"greedy decode of one token at position {self.n_keys - 1}: 28 "
+                            "Qwen3-0.6B layers (fused Q8_0 projections, norms, SwiGLU, attention "
+                            "over the cache) + output norm + LM head + argmax",
+                "layers": self.layers, "n_keys": self.n_keys, "hidden": self.hid,
+                "vocab": self.vocab, "bytes_per_token": self.work_per_call}
+
+
+class Token32k(Token):
+    name = "token32k"
+
+
+class Token512(Token):
+    name = "token512"
+    n_keys = 513
+
+
 WORKLOADS = {c.name: c for c in (Decode32k, Prefill2k, Ragged, Chunk32k, Decode512, Copy,
-                                 Q8LmHead, Q8Proj)}
+                                 Q8LmHead, Q8Proj, Token32k, Token512)}
 
 
 def settle_clocks(torch, w, seconds=0.5):
@@ -511,8 +596,11 @@ def run(torch, ops, stream, name, steps, warmup):
     out = {"value": round(value, 3), "unit": w.unit, "ms_per_step": round(ms, 4),
            "config": w.config(),
            "roofline": w.roofline(call_ms, traffic_from_profiles(f"{name}_pmc.md"))}
+    if hasattr(w, "extra"):
+        out.update(w.extra(ms))
     # Drop the device buffers; the CPU baseline needs only the sizes.
-    for k in [k for k, v in vars(w).items() if isinstance(v, (torch.Tensor, list, ops.Workspace))]:
+    for k in [k for k, v in vars(w).items()
+              if isinstance(v, (torch.Tensor, list, ops.Workspace, ops.DeviceBuffer, ops.Q8Matrix))]:
         delattr(w, k)
     torch.cuda.empty_cache()
     return out, w.cpu_baseline
@@ -552,6 +640,9 @@ def main():
                "data": "synthetic: seeded N(0,1) q/k/v and K/V caches, norm gains N(1,0.1); "
                        "no weights (attention path only)",
                "config": main_res["config"], "roofline": main_res["roofline"]}
+        for k in ("tokens_per_s", "ms_per_token"):
+            if k in main_res:
+                out[k] = main_res[k]
         if main_res["unit"] == "GB/s":
             out["frac_of_hbm_peak"] = round(main_res["value"] / HBM_PEAK_GBS, 4)
         else:

@@ -150,9 +150,11 @@ class DecoderLayer:
             raise DesyncError(f"desync: offset {offset} but the cache holds {self.nKeys} keys")
 
     # ------------------------------------------------------------------ decode
-    def encode(self, hidden=None, offset: int | None = None) -> None:
+    def encode(self, hidden=None, offset: int | None = None, src=None) -> None:
         """One decode step at position nKeys (layer.ts:571-654). ``hidden``
-        omitted: consume the previous step's output (layer.ts:645-648)."""
+        omitted: consume the previous step's output (layer.ts:645-648);
+        ``src``: read the input from that device buffer instead (the previous
+        layer's ``outputBuffer()``, no copy)."""
         cfg, b, g = self.cfg, self.buf, self.g
         H, Hkv, d = cfg.nHeads, cfg.nKvHeads, cfg.headDim
         pos = self.nKeys
@@ -160,14 +162,15 @@ class DecoderLayer:
         if pos >= cfg.maxKeys:
             raise CacheFullError(-2, f"KV cache full at {cfg.maxKeys} keys")
         self._hidden_in(1, hidden)
+        hin = b["h"] if src is None else src
         qkv = b["qkv"].ptr
-        ops.q8_matvec_ex(self.w_qkv, b["h"], b["qkv"], 1, norm_gain=g["attn_norm.weight"],
+        ops.q8_matvec_ex(self.w_qkv, hin, b["qkv"], 1, norm_gain=g["attn_norm.weight"],
                          eps=cfg.eps)
         ops.decode_layer(qkv, qkv + H * d * 4, qkv + (H + Hkv) * d * 4, g["attn_q_norm.weight"],
                          g["attn_k_norm.weight"], b["invFreq"], cfg.eps, cfg.ropePairing,
                          b["qn"], b["kcache"], b["vcache"], b["attn"], pos, H, Hkv, d,
                          cfg.maxKeys, self.ws)
-        ops.q8_matvec_ex(self.w_o, b["attn"], b["h2"], 1, res=b["h"])
+        ops.q8_matvec_ex(self.w_o, b["attn"], b["h2"], 1, res=hin)
         ops.q8_matvec_ex(self.w_gu, b["h2"], b["gu"], 1, norm_gain=g["ffn_norm.weight"],
                          eps=cfg.eps)
         ops.q8_matvec_ex(self.w_down, b["gu"], b["out"], 1, up=b["gu"].ptr + cfg.ffn * 4,
@@ -209,6 +212,10 @@ class DecoderLayer:
         self.buf["h"], self.buf["out"] = self.buf["out"], self.buf["h"]
 
     # ----------------------------------------------------------------- readout
+    def outputBuffer(self) -> ops.DeviceBuffer:
+        """The device buffer holding the last call's output (the next layer's input)."""
+        return self.buf["h"]
+
     def readOutput(self, nTokens: int = 1) -> np.ndarray:
         """The layer output of the last encode / encodePrefill (synchronous)."""
         return self.buf["h"].download(nTokens * self.cfg.hidden)
