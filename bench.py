@@ -30,6 +30,10 @@ of the hot path over one batch of synthetic, HBM-resident input:
              layers (DecoderLayer: fused projections + attention over 32769
              keys) + output norm + LM head + argmax. GB/s and tokens/s.
   token512   The same at 513 keys (launch-bound).
+  gen32k     Greedy generation with the captured one-token HIP graph
+             (flock_amd.model): 32 tokens per step from position 32768.
+             GB/s and tokens/s.
+  gen512     The same from position 512.
 
 The default run also measures prefill2k (the metric's second half) and reports
 it under "prefill", and the LM-head projection under "q8_lm_head". Inputs are N(0, 1) from a seeded generator (gains
@@ -542,8 +546,85 @@ class Token512(Token):
     n_keys = 513
 
 
+class Gen(Workload):
+    """Greedy generation through the whole model with the captured one-token
+    HIP graph (flock_amd.model.Model.replay): 28 Qwen3-0.6B layers + head, the
+    position, fed-back token and token log on the device. A step is 32 tokens
+    decoded from position n_keys - 1 (the caches are rewound between steps)."""
+
+    unit = "GB/s"
+    kernel = "Model.replay: one hipGraphLaunch per token (embed, 28 x 6 kernels, head, advance)"
+    n_keys = 32769
+    tokens = 32
+
+    def __init__(self, torch, ops):
+        from flock_amd.decoder import DecoderConfig
+        from flock_amd.model import Model
+        self.torch, self.ops = torch, ops
+        rng = np.random.default_rng(13)
+        cfg = DecoderConfig(maxKeys=self.n_keys + self.tokens, maxPrefill=1)
+        log(f"[{self.name}] building the model (random Q8_0 weights)")
+
+        def packed(rows, cols, scale=8e-4):
+            blocks = np.empty((rows * cols // 32, 34), np.uint8)
+            blocks[:, :2] = (rng.random(blocks.shape[0]) * scale + 1e-5).astype(
+                np.float16).view(np.uint8).reshape(-1, 2)
+            blocks[:, 2:] = rng.integers(0, 256, (blocks.shape[0], 32), dtype=np.uint8)
+            return blocks.ravel()
+
+        layers = []
+        for _ in range(28):
+            w = {n: packed(r, c) for n, (r, c) in cfg.shapes().items()}
+            for n, sz in (("attn_norm.weight", cfg.hidden), ("ffn_norm.weight", cfg.hidden),
+                          ("attn_q_norm.weight", cfg.headDim), ("attn_k_norm.weight", cfg.headDim)):
+                w[n] = (1 + 0.1 * rng.standard_normal(sz)).astype(np.float32)
+            layers.append(w)
+        self.vocab = 151936
+        self.model = Model(cfg, layers, packed(self.vocab, cfg.hidden, 0.02),
+                           (1 + 0.1 * rng.standard_normal(cfg.hidden)).astype(np.float32),
+                           self.vocab, max_generate=self.tokens)
+        del layers
+        for layer in self.model.layers:
+            layer.buf["kcache"].zero()
+            layer.buf["vcache"].zero()
+        layer_w = sum(r * c * 34 // 32 for r, c in cfg.shapes().values())
+        kv = 2 * self.n_keys * cfg.nKvHeads * cfg.headDim * 4
+        self.work_per_token = 28 * (layer_w + kv) + self.vocab * cfg.hidden * 34 // 32
+        self.work_per_step = self.tokens * self.work_per_token
+        self.work_per_call = self.work_per_step
+        self.calls_per_step = 1
+
+    def call(self, l=0):
+        m = self.model
+        m.nKeys = self.n_keys - 1
+        m.replay(17, self.tokens, read=False)
+
+    def step(self):
+        self.call()
+
+    def extra(self, ms):
+        return {"tokens_per_s": round(self.tokens * 1e3 / ms, 2),
+                "ms_per_token": round(ms / self.tokens, 4)}
+
+    def config(self):
+        return {"workload": f"greedy generation, {self.tokens} tokens per step from position "
+                            f"{self.n_keys - 1}: 28 Qwen3-0.6B layers + head per token, one HIP "
+                            "graph replay per token", "layers": 28, "n_keys": self.n_keys,
+                "tokens_per_step": self.tokens, "vocab": self.vocab,
+                "bytes_per_token": self.work_per_token}
+
+
+class Gen32k(Gen):
+    name = "gen32k"
+
+
+class Gen512(Gen):
+    name = "gen512"
+    n_keys = 513
+
+
 WORKLOADS = {c.name: c for c in (Decode32k, Prefill2k, Ragged, Chunk32k, Decode512, Copy,
-                                 Q8LmHead, Q8Proj, Token32k, Token512)}
+                                 Q8LmHead, Q8Proj, Token32k, Token512, Gen32k, Gen512)}
 
 
 def settle_clocks(torch, w, seconds=0.5):
@@ -599,8 +680,11 @@ def run(torch, ops, stream, name, steps, warmup):
     if hasattr(w, "extra"):
         out.update(w.extra(ms))
     # Drop the device buffers; the CPU baseline needs only the sizes.
+    if hasattr(w, "model"):
+        w.model.free()
     for k in [k for k, v in vars(w).items()
-              if isinstance(v, (torch.Tensor, list, ops.Workspace, ops.DeviceBuffer, ops.Q8Matrix))]:
+              if isinstance(v, (torch.Tensor, list, ops.Workspace, ops.DeviceBuffer, ops.Q8Matrix))
+              or k == "model"]:
         delattr(w, k)
     torch.cuda.empty_cache()
     return out, w.cpu_baseline

@@ -62,8 +62,21 @@ SIGNATURES: dict[str, tuple] = {
     "flk_q8_matvec": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32]),
     "flk_q8_split": (_i32, [_p, _u32, _u32, _p, _p]),
     "flk_q8_matvec_ex": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32, _p, _f32, _p, _p]),
+    "flk_q8_gate_up_swiglu": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32, _p, _f32]),
     "flk_swiglu": (_i32, [_p, _p, _p, _u32]),
     "flk_add": (_i32, [_p, _p, _p, _u32]),
+    # include/flock_graph.h
+    "flk_decode_layer_dev": (
+        _i32,
+        [_p, _p, _p, _p, _p, _p, _f32, _i32, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _p, _u64]),
+    "flk_embed": (_i32, [_p, _p, _p, _u32, _u32, _u32, _p]),
+    "flk_advance": (_i32, [_p, _u32, _p, _p, _u32]),
+    "flk_stream_create": (_i32, [ctypes.POINTER(_p)]),
+    "flk_stream_destroy": (_i32, [_p]),
+    "flk_capture_begin": (_i32, []),
+    "flk_capture_end": (_i32, [ctypes.POINTER(_p)]),
+    "flk_graph_launch": (_i32, [_p]),
+    "flk_graph_destroy": (_i32, [_p]),
     # include/flock_wire.h
     "flk_f32_to_f16": (_i32, [_p, _p, _u64]),
     "flk_f16_to_f32": (_i32, [_p, _p, _u64]),

@@ -286,11 +286,13 @@ int32_t flk_attn_prefill(const float* q, const float* kcache, const float* vcach
                     "flk_attn_prefill");
 }
 
-int32_t flk_decode_layer(const float* q_raw, const float* k_raw, const float* v_raw,
-                         const float* gq, const float* gk, const float* inv_freq, float eps,
-                         int32_t pairing, float* qn_out, float* kcache, float* vcache, float* o,
-                         uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                         uint32_t max_keys, void* ws, uint64_t ws_bytes) {
+static int32_t decode_layer_common(const float* q_raw, const float* k_raw, const float* v_raw,
+                                   const float* gq, const float* gk, const float* inv_freq,
+                                   float eps, int32_t pairing, float* qn_out, float* kcache,
+                                   float* vcache, float* o, uint32_t n_keys,
+                                   const uint32_t* n_keys_dev, uint32_t n_heads,
+                                   uint32_t n_kv_heads, uint32_t head_dim, void* ws,
+                                   uint64_t ws_bytes, const char* what) {
   FLK_NONNULL(q_raw);
   FLK_NONNULL(k_raw);
   FLK_NONNULL(v_raw);
@@ -309,8 +311,7 @@ int32_t flk_decode_layer(const float* q_raw, const float* k_raw, const float* v_
   if (rc) return rc;
   if (pairing != FLK_ROPE_NEOX && pairing != FLK_ROPE_NORM)
     return fail(FLK_ERR_ARG, "rope pairing %d (0 = neox, 1 = norm)", pairing);
-  if (pos >= max_keys) return fail(FLK_ERR_CACHE_FULL, "KV cache full at %u keys", max_keys);
-  const DecodeShape s{n_heads, n_kv_heads, head_dim, 1, pos + 1};
+  const DecodeShape s{n_heads, n_kv_heads, head_dim, 1, n_keys};
   rc = check_ws(ws, ws_bytes, decode_ws_bytes(s));
   if (rc) return rc;
   DecodeFused f;
@@ -325,8 +326,33 @@ int32_t flk_decode_layer(const float* q_raw, const float* k_raw, const float* v_
   f.qn_out = qn_out;
   f.kcache_w = kcache;
   f.vcache_w = vcache;
-  return hip_status(launch_decode(qn_out, kcache, vcache, o, nullptr, nullptr, s, &f, ws, g_stream),
-                    "flk_decode_layer");
+  return hip_status(launch_decode(qn_out, kcache, vcache, o, nullptr, n_keys_dev, s, &f, ws,
+                                  g_stream),
+                    what);
+}
+
+int32_t flk_decode_layer(const float* q_raw, const float* k_raw, const float* v_raw,
+                         const float* gq, const float* gk, const float* inv_freq, float eps,
+                         int32_t pairing, float* qn_out, float* kcache, float* vcache, float* o,
+                         uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                         uint32_t max_keys, void* ws, uint64_t ws_bytes) {
+  if (pos >= max_keys) return fail(FLK_ERR_CACHE_FULL, "KV cache full at %u keys", max_keys);
+  return decode_layer_common(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
+                             vcache, o, pos + 1, nullptr, n_heads, n_kv_heads, head_dim, ws,
+                             ws_bytes, "flk_decode_layer");
+}
+
+int32_t flk_decode_layer_dev(const float* q_raw, const float* k_raw, const float* v_raw,
+                             const float* gq, const float* gk, const float* inv_freq, float eps,
+                             int32_t pairing, float* qn_out, float* kcache, float* vcache,
+                             float* o, const uint32_t* n_keys_dev, uint32_t n_heads,
+                             uint32_t n_kv_heads, uint32_t head_dim, uint32_t max_keys, void* ws,
+                             uint64_t ws_bytes) {
+  FLK_NONNULL(n_keys_dev);
+  if (max_keys == 0) return fail(FLK_ERR_ARG, "decode_layer_dev max_keys 0");
+  return decode_layer_common(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
+                             vcache, o, max_keys, n_keys_dev, n_heads, n_kv_heads, head_dim, ws,
+                             ws_bytes, "flk_decode_layer_dev");
 }
 
 int32_t flk_attn_decode_ragged(const float* q, const float* kcache, const float* vcache,
@@ -453,6 +479,35 @@ int32_t flk_q8_matvec_ex(const int8_t* qs, const uint16_t* scales, const float* 
                     "flk_q8_matvec_ex");
 }
 
+int32_t flk_q8_gate_up_swiglu(const int8_t* qs, const uint16_t* scales, const float* x,
+                              float* act, uint32_t n_ffn, uint32_t n_cols, uint32_t n_tokens,
+                              const float* norm_gain, float norm_eps) {
+  FLK_NONNULL(qs);
+  FLK_NONNULL(scales);
+  FLK_NONNULL(x);
+  FLK_NONNULL(act);
+  if (n_ffn == 0 || n_cols == 0 || n_tokens == 0 || n_cols % 32 != 0)
+    return fail(FLK_ERR_ARG, "gate_up_swiglu n_ffn=%u n_cols=%u n_tokens=%u", n_ffn, n_cols,
+                n_tokens);
+  if (n_cols > 1024)
+    return fail(FLK_ERR_UNSUPPORTED, "gate_up_swiglu needs n_cols <= 1024 (got %u)", n_cols);
+  if (n_tokens > 65535) return fail(FLK_ERR_UNSUPPORTED, "q8_matvec n_tokens %u > 65535", n_tokens);
+  if (norm_gain != nullptr && !(norm_eps >= 0.f))
+    return fail(FLK_ERR_ARG, "gate_up_swiglu: eps must be >= 0");
+  FLK_ALIGNED(qs);
+  FLK_ALIGNED(x);
+  if (reinterpret_cast<uintptr_t>(scales) % 2 != 0)
+    return fail(FLK_ERR_ARG, "scales must be 2-byte aligned");
+  Q8Fuse f;
+  f.norm_gain = norm_gain;
+  f.norm_eps = norm_eps;
+  f.act = act;
+  return hip_status(launch_q8_matvec(reinterpret_cast<const uint8_t*>(qs), scales, x, nullptr,
+                                     2 * n_ffn, n_cols, n_tokens, g_stream, nullptr, nullptr,
+                                     nullptr, &f),
+                    "flk_q8_gate_up_swiglu");
+}
+
 int32_t flk_swiglu(const float* gate, const float* up, float* o, uint32_t n) {
   FLK_NONNULL(gate);
   FLK_NONNULL(up);
@@ -541,4 +596,73 @@ int32_t flk_wire_header_unpack(const void* frame, uint64_t frame_bytes, uint32_t
   if (flags) *flags = get_u32(p + 16);
   if (n_values) *n_values = (frame_bytes - FLK_WIRE_HEADER_BYTES) / 2;
   return FLK_OK;
+}
+
+// ----------------------------------------------------------------- graph ---
+int32_t flk_embed(const int8_t* qs, const uint16_t* scales, const uint32_t* ids,
+                  uint32_t n_tokens, uint32_t vocab, uint32_t hidden, float* out) {
+  FLK_NONNULL(qs);
+  FLK_NONNULL(scales);
+  FLK_NONNULL(ids);
+  FLK_NONNULL(out);
+  if (n_tokens == 0 || vocab == 0 || hidden == 0 || hidden % 32 != 0)
+    return fail(FLK_ERR_ARG, "embed n_tokens=%u vocab=%u hidden=%u (a multiple of 32)", n_tokens,
+                vocab, hidden);
+  if (reinterpret_cast<uintptr_t>(qs) % 4 != 0 || reinterpret_cast<uintptr_t>(scales) % 2 != 0)
+    return fail(FLK_ERR_ARG, "embed: qs must be 4-byte and scales 2-byte aligned");
+  FLK_ALIGNED(out);
+  return hip_status(launch_embed(qs, scales, ids, n_tokens, vocab, hidden, out, g_stream),
+                    "flk_embed");
+}
+
+int32_t flk_advance(uint32_t* state, uint32_t delta, const uint32_t* value, uint32_t* log,
+                    uint32_t log_len) {
+  FLK_NONNULL(state);
+  return hip_status(launch_advance(state, delta, value, log, log_len, g_stream), "flk_advance");
+}
+
+int32_t flk_stream_create(void** stream) {
+  FLK_NONNULL(stream);
+  hipStream_t s = nullptr;
+  int32_t rc = hip_status(hipStreamCreateWithFlags(&s, hipStreamNonBlocking), "hipStreamCreate");
+  *stream = rc ? nullptr : s;
+  return rc;
+}
+
+int32_t flk_stream_destroy(void* stream) {
+  if (stream == nullptr) return FLK_OK;
+  if (g_stream == static_cast<hipStream_t>(stream)) g_stream = nullptr;
+  return hip_status(hipStreamDestroy(static_cast<hipStream_t>(stream)), "hipStreamDestroy");
+}
+
+int32_t flk_capture_begin(void) {
+  if (g_stream == nullptr)
+    return fail(FLK_ERR_ARG, "capture needs a stream (flk_set_stream), not the null stream");
+  return hip_status(hipStreamBeginCapture(g_stream, hipStreamCaptureModeRelaxed),
+                    "hipStreamBeginCapture");
+}
+
+int32_t flk_capture_end(void** graph) {
+  FLK_NONNULL(graph);
+  *graph = nullptr;
+  hipGraph_t g = nullptr;
+  int32_t rc = hip_status(hipStreamEndCapture(g_stream, &g), "hipStreamEndCapture");
+  if (rc) return rc;
+  hipGraphExec_t exec = nullptr;
+  rc = hip_status(hipGraphInstantiate(&exec, g, nullptr, nullptr, 0), "hipGraphInstantiate");
+  (void)hipGraphDestroy(g);  // the executable graph keeps what it needs
+  if (rc) return rc;
+  *graph = exec;
+  return FLK_OK;
+}
+
+int32_t flk_graph_launch(void* graph) {
+  FLK_NONNULL(graph);
+  return hip_status(hipGraphLaunch(static_cast<hipGraphExec_t>(graph), g_stream),
+                    "hipGraphLaunch");
+}
+
+int32_t flk_graph_destroy(void* graph) {
+  if (graph == nullptr) return FLK_OK;
+  return hip_status(hipGraphExecDestroy(static_cast<hipGraphExec_t>(graph)), "hipGraphExecDestroy");
 }

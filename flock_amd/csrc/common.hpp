@@ -7,6 +7,7 @@
 #include "../../include/flock_attn.h"
 #include "../../include/flock_q8.h"
 #include "../../include/flock_wire.h"
+#include "../../include/flock_graph.h"
 #include "trig.hpp"
 
 namespace flk {
@@ -244,6 +245,7 @@ struct Q8Fuse {
   float norm_eps = 0.f;
   const float* up = nullptr;         // x <- swiglu(x, up)
   const float* res = nullptr;        // o <- res + W x
+  float* act = nullptr;              // (gate, up) row pairs -> act = swiglu (<= 1024 columns)
 };
 hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const float* x, float* o,
                             uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens, hipStream_t st,
@@ -254,6 +256,12 @@ uint32_t q8_max_workgroups(uint32_t n_rows, uint32_t n_cols);
 // op 0: swiglu(a, b); op 1: a + b (elementwise.wgsl).
 hipError_t launch_elementwise(int op, const float* a, const float* b, float* o, uint32_t n,
                               hipStream_t st);
+
+hipError_t launch_embed(const int8_t* qs, const uint16_t* scales, const uint32_t* ids,
+                        uint32_t n_tokens, uint32_t vocab, uint32_t hidden, float* out,
+                        hipStream_t st);
+hipError_t launch_advance(uint32_t* state, uint32_t delta, const uint32_t* value, uint32_t* log,
+                          uint32_t log_len, hipStream_t st);
 
 // dir 0: f32 -> f16 (wire pack), 1: f16 -> f32 (wire unpack).
 hipError_t launch_wire(int dir, const void* in, void* out, uint64_t n, hipStream_t st);

@@ -19,7 +19,19 @@ __global__ __launch_bounds__(128) void rmsnorm_kernel(const float* __restrict__ 
   if (vec >= n_vecs) return;  // uniform per block
   const float* xv = x + (size_t)vec * n;
   float acc = 0.f;
-  for (uint32_t i = t; i < n; i += 128) acc = fma32(xv[i], xv[i], acc);
+  // Eight elements are loaded before any is used; past the end they read 0,
+  // which adds exactly nothing to the partial.
+  for (uint32_t base = t; base < n; base += 128 * 8) {
+    float v[8];
+#pragma unroll
+    for (int k = 0; k < 8; k++) {
+      const uint32_t i = base + 128 * k;
+      v[k] = xv[min(i, n - 1)];
+      v[k] = i < n ? v[k] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < 8; k++) acc = fma32(v[k], v[k], acc);
+  }
   part[t] = acc;
   __syncthreads();
   for (uint32_t stride = 64; stride > 0; stride >>= 1) {

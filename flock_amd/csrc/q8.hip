@@ -51,41 +51,83 @@ struct Q8Args {
   float norm_eps;
   const float* up;          // x <- swiglu(x, up) (elementwise.wgsl:24-30; x is the gate)
   const float* res;         // o <- res + W x (elementwise.wgsl:32-37, the residual add)
+  // Rows in (gate, up) pairs: 2i = gate row i, 2i + 1 = up row i. Instead of
+  // o, act[t][i] = swiglu(gate_i, up_i) (elementwise.wgsl:24-30). Needs two
+  // or more rows per wave (at most 1024 columns).
+  float* act;
 };
 
-// The matvec input element i of token tok after the optional fusion:
-// rmsnorm: fr(fr(x * scale) * g) (rmsnorm.wgsl:67-72); swiglu:
-// fr(fr(g / fr(1 + fr(exp(-g)))) * up) with exp in f64 and rounded once
-// (swigluRef, ops_ref.ts:103-110).
-__device__ __forceinline__ float q8_xin(const Q8Args& a, const float* xt, size_t tok_off,
-                                        uint32_t i, float scale) {
-  const float v = xt[i];
-  if (a.norm_gain != nullptr) return (v * scale) * a.norm_gain[i];
-  if (a.up != nullptr) {
-    const float e = (float)exp(-(double)v);
-    return (v / (1.f + e)) * a.up[tok_off + i];
-  }
-  return v;
+// swigluRef (ops_ref.ts:103-110): fr(fr(g / fr(1 + fr(exp(-g)))) * up).
+__device__ __forceinline__ float q8_swiglu(float g, float u) {
+  const float e = (float)exp(-(double)g);
+  return (g / (1.f + e)) * u;
 }
 
-// rmsnorm scale of token tok's x (rmsnorm.wgsl:45-66): 128 strided fma32
-// partials, pairwise LDS tree, scale = 1 / sqrt(mean + eps) rounded once. Every
-// thread of the workgroup must call it; returns 1 when there is no norm.
+// Fused inputs c0 .. c0 + 31 of one token (xt: the token's x, tok_off: its
+// offset in x and up).
+__device__ __forceinline__ void q8_fused_block(const Q8Args& a, const float* xt, size_t tok_off,
+                                               uint32_t c0, float scale, float (&out)[32]) {
+  float4 xv[8], yv[8];
+  const float4* xs = reinterpret_cast<const float4*>(xt + c0);
+#pragma unroll
+  for (int i = 0; i < 8; i++) xv[i] = xs[i];
+  if (a.norm_gain != nullptr) {  // uniform
+    const float4* gs = reinterpret_cast<const float4*>(a.norm_gain + c0);
+#pragma unroll
+    for (int i = 0; i < 8; i++) yv[i] = gs[i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      out[4 * i + 0] = (xv[i].x * scale) * yv[i].x;
+      out[4 * i + 1] = (xv[i].y * scale) * yv[i].y;
+      out[4 * i + 2] = (xv[i].z * scale) * yv[i].z;
+      out[4 * i + 3] = (xv[i].w * scale) * yv[i].w;
+    }
+  } else {
+    const float4* us = reinterpret_cast<const float4*>(a.up + tok_off + c0);
+#pragma unroll
+    for (int i = 0; i < 8; i++) yv[i] = us[i];
+#pragma unroll
+    for (int i = 0; i < 8; i++) {
+      out[4 * i + 0] = q8_swiglu(xv[i].x, yv[i].x);
+      out[4 * i + 1] = q8_swiglu(xv[i].y, yv[i].y);
+      out[4 * i + 2] = q8_swiglu(xv[i].z, yv[i].z);
+      out[4 * i + 3] = q8_swiglu(xv[i].w, yv[i].w);
+    }
+  }
+}
+
+// rmsnorm scale of a token's x (rmsnorm.wgsl:45-66), per wave and without a
+// barrier: lane l holds the reference's partials l and l + 64 (stride-128
+// fma32 sums), their sum is the tree's stride-64 step, and the xor butterfly
+// over the wave is its strides 32 .. 1; scale = 1 / sqrt(mean + eps) rounded
+// once. (A workgroup barrier would also wait for the weight loads already in
+// flight.) Returns 1 when there is no norm.
 __device__ __forceinline__ float q8_norm_scale(const Q8Args& a, const float* xt) {
   if (a.norm_gain == nullptr) return 1.f;
-  __shared__ float part[128];
-  const uint32_t t = threadIdx.x;
-  if (t < 128) {
-    float acc = 0.f;
-    for (uint32_t i = t; i < a.n_cols; i += 128) acc = fma32(xt[i], xt[i], acc);
-    part[t] = acc;
+  const uint32_t l = threadIdx.x & 63;
+  // Elements l + 64k: even k feed partial l, odd k partial l + 64. Eight are
+  // loaded before any is used (a load-use loop would serialise the
+  // latencies); past the end they read 0, which adds exactly nothing.
+  constexpr int kB = 8;
+  float p0 = 0.f, p1 = 0.f;
+  for (uint32_t base = l; base < a.n_cols; base += 64 * kB) {
+    float v[kB];
+#pragma unroll
+    for (int k = 0; k < kB; k++) {
+      const uint32_t i = base + 64 * k;
+      v[k] = xt[min(i, a.n_cols - 1)];
+      v[k] = i < a.n_cols ? v[k] : 0.f;
+    }
+#pragma unroll
+    for (int k = 0; k < kB; k += 2) {
+      p0 = fma32(v[k], v[k], p0);
+      p1 = fma32(v[k + 1], v[k + 1], p1);
+    }
   }
-  __syncthreads();
-  for (uint32_t stride = 64; stride > 0; stride >>= 1) {
-    if (t < stride) part[t] = part[t] + part[t + stride];
-    __syncthreads();
-  }
-  const float mean = part[0] / (float)a.n_cols;
+  float sum = p0 + p1;
+#pragma unroll
+  for (int m = 32; m >= 1; m >>= 1) sum += shfl_xor(sum, m);
+  const float mean = sum / (float)a.n_cols;
   return rsqrt_once(mean + a.norm_eps);
 }
 
@@ -124,6 +166,28 @@ __device__ __forceinline__ float q8_block(float part, float scale, uint4 w0, uin
   return part;
 }
 
+// Weights of kQ8Unroll row groups g0, g0 + waves, ... for logical lane ll of
+// row slot sub (rows past the end re-read the last row, so every load is
+// unconditional).
+template <int P, int NB, int UR>
+__device__ __forceinline__ void q8_load_rows(const Q8Args& a, uint32_t g0, uint32_t waves, int ll,
+                                             int sub, uint32_t nb, uint4 (&w0)[UR][NB],
+                                             uint4 (&w1)[UR][NB], uint16_t (&hs)[UR][NB]) {
+  constexpr int R = kWave / P;
+#pragma unroll
+  for (int u = 0; u < UR; u++) {
+    const uint32_t row = min((g0 + waves * u) * R + sub, a.n_rows - 1);
+#pragma unroll
+    for (int j = 0; j < NB; j++) {
+      const uint32_t b = min((uint32_t)(ll + kQ8Lanes * j), nb - 1);
+      const uint4* src = reinterpret_cast<const uint4*>(a.qs + (size_t)row * a.n_cols + 32 * (size_t)b);
+      w0[u][j] = src[0];
+      w1[u][j] = src[1];
+      hs[u][j] = a.scales[(size_t)row * nb + b];
+    }
+  }
+}
+
 // P logical lanes per row, NB x blocks per lane in registers (NB * 64 >= the
 // row's block count). Grid: (workgroups over row groups, tokens).
 // FUSE: the input fusions (rmsnorm / swiglu) are compiled in.
@@ -138,6 +202,12 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
   const uint32_t nb = a.n_cols / 32;
   const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
   const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
+
+  // The first row groups' weights are requested before x is prepared, so
+  // the input fusion's latency (the norm's reduction) overlaps their fetch.
+  uint4 w0[kQ8Unroll][NB], w1[kQ8Unroll][NB];
+  uint16_t hs[kQ8Unroll][NB];
+  q8_load_rows<P, NB, kQ8Unroll>(a, wave, waves, ll, sub, nb, w0, w1, hs);
 
   // x blocks ll, ll + 64, ... of this token (zeros past the row's end),
   // after the optional input fusion.
@@ -162,8 +232,9 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
         xr[j][4 * i + 3] = v.w;
       }
     } else {
-#pragma unroll
-      for (int i = 0; i < 32; i++) xr[j][i] = q8_xin(a, xt, tok_off, c0 + i, scale);
+      // Every load of the block first (float4s), then the arithmetic: a
+      // per-element load-then-use sequence serialises 32 memory latencies.
+      q8_fused_block(a, xt, tok_off, c0, scale, xr[j]);
     }
   }
 
@@ -173,22 +244,9 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
 
   const uint32_t n_groups = (a.n_rows + R - 1) / R;
   for (uint32_t g0 = wave; g0 < n_groups; g0 += waves * kQ8Unroll) {
-    // Loads of kQ8Unroll row groups first (rows past the end re-read the last
-    // row, so every load is unconditional), then the arithmetic.
-    uint4 w0[kQ8Unroll][NB], w1[kQ8Unroll][NB];
-    uint16_t hs[kQ8Unroll][NB];
-#pragma unroll
-    for (int u = 0; u < kQ8Unroll; u++) {
-      const uint32_t row = min((g0 + waves * u) * R + sub, a.n_rows - 1);
-#pragma unroll
-      for (int j = 0; j < NB; j++) {
-        const uint32_t b = min((uint32_t)(ll + kQ8Lanes * j), nb - 1);
-        const uint4* src = reinterpret_cast<const uint4*>(a.qs + (size_t)row * a.n_cols + 32 * (size_t)b);
-        w0[u][j] = src[0];
-        w1[u][j] = src[1];
-        hs[u][j] = a.scales[(size_t)row * nb + b];
-      }
-    }
+    // Loads of kQ8Unroll row groups first, then the arithmetic (the first
+    // groups were loaded above).
+    if (g0 != wave) q8_load_rows<P, NB, kQ8Unroll>(a, g0, waves, ll, sub, nb, w0, w1, hs);
 #pragma unroll
     for (int u = 0; u < kQ8Unroll; u++) {
       float part = 0.f;
@@ -199,6 +257,12 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
 #pragma unroll
       for (int m = P / 2; m >= 1; m >>= 1) part += shfl_xor(part, m);
       const uint32_t row = (g0 + waves * u) * R + sub;
+      if (R >= 2 && a.act != nullptr) {  // uniform: (gate, up) row pairs -> SwiGLU
+        const float up = shfl_xor(part, R >= 2 ? P : 0);  // the odd row of the pair
+        if (ll == 0 && (sub & 1) == 0 && g0 + waves * u < n_groups && row + 1 < a.n_rows)
+          a.act[(size_t)tok * (a.n_rows / 2) + row / 2] = q8_swiglu(part, up);
+        continue;
+      }
       if (ll == 0 && g0 + waves * u < n_groups && row < a.n_rows) {
         const size_t oi = (size_t)tok * a.n_rows + row;
         if (a.res != nullptr) part = a.res[oi] + part;
@@ -231,8 +295,19 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
     for (uint32_t b = lane; b < nb; b += kQ8Lanes) {
       const uint4* src = reinterpret_cast<const uint4*>(a.qs + (size_t)row * a.n_cols + 32 * (size_t)b);
       float xb[32];
+      if (a.norm_gain == nullptr && a.up == nullptr) {
+        const float4* xs = reinterpret_cast<const float4*>(xt + 32 * (size_t)b);
 #pragma unroll
-      for (int i = 0; i < 32; i++) xb[i] = q8_xin(a, xt, tok_off, 32 * b + i, scale);
+        for (int i = 0; i < 8; i++) {
+          const float4 v = xs[i];
+          xb[4 * i + 0] = v.x;
+          xb[4 * i + 1] = v.y;
+          xb[4 * i + 2] = v.z;
+          xb[4 * i + 3] = v.w;
+        }
+      } else {
+        q8_fused_block(a, xt, tok_off, 32 * b, scale, xb);
+      }
       part = q8_block(part, q8_scale(a.scales[(size_t)row * nb + b]), src[0], src[1], xb);
     }
 #pragma unroll
@@ -311,12 +386,13 @@ hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const flo
                             hipStream_t st, float* best_val, uint32_t* best_idx,
                             uint32_t* n_workgroups, const Q8Fuse* fuse) {
   Q8Args a{qs, scales, x, o, n_rows, n_cols, n_tokens, best_val, best_idx,
-           nullptr, 0.f, nullptr, nullptr};
+           nullptr, 0.f, nullptr, nullptr, nullptr};
   if (fuse != nullptr) {
     a.norm_gain = fuse->norm_gain;
     a.norm_eps = fuse->norm_eps;
     a.up = fuse->up;
     a.res = fuse->res;
+    a.act = fuse->act;
   }
   const uint32_t nb = n_cols / 32;
   uint32_t gx;

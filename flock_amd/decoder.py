@@ -13,14 +13,17 @@ Q8_0 projections as GGUF 34-byte blocks (``attn_q.weight``, ``attn_k.weight``,
 ``ffn_norm.weight``, ``attn_q_norm.weight``, ``attn_k_norm.weight``).
 
 Launches per decode step (the reference dispatches ~16): the norms, residual
-adds and SwiGLU ride inside the projections (``flk_q8_matvec_ex``), q/k/v are
-one projection over the row-stacked matrix and so are gate/up:
+adds and SwiGLU ride inside the projections, q/k/v are one projection over
+the row-stacked matrix, gate/up one over the row-interleaved matrix:
 
-  1. qkv = W_qkv rmsnorm(h)              flk_q8_matvec_ex (norm fused)
-  2. attention slice                     flk_decode_layer (2 kernels)
-  3. h2 = h + W_o attn                   flk_q8_matvec_ex (residual fused)
-  4. gu = W_gateup rmsnorm(h2)           flk_q8_matvec_ex (norm fused)
-  5. out = h2 + W_down swiglu(gate, up)  flk_q8_matvec_ex (swiglu + residual)
+  1. qkv = W_qkv rmsnorm(h)                 flk_q8_matvec_ex (norm fused)
+  2. attention slice                        flk_decode_layer (2 kernels)
+  3. h2 = h + W_o attn                      flk_q8_matvec_ex (residual fused)
+  4. act = swiglu(W_gate|up rmsnorm(h2))    flk_q8_gate_up_swiglu (norm fused)
+  5. out = h2 + W_down act                  flk_q8_matvec_ex (residual fused)
+
+(hidden > 1024: gate/up stacked, SwiGLU computed as the down projection
+loads its input.)
 
 Every op keeps the reference's arithmetic, so the K/V rows this layer writes
 are bit-identical to layerForwardRef's and the output differs from it only
@@ -96,16 +99,26 @@ class DecoderLayer:
             sc = np.concatenate([split[n][1] for n in names])
             return ops.Q8Matrix(qs, sc, sum(shapes[n][0] for n in names), shapes[names[0]][1])
 
-        # q|k|v and gate|up stacked row-wise: one launch each (same bits per row).
+        # q|k|v stacked row-wise: one launch (same bits per row).
         self.w_qkv = stack(("attn_q.weight", "attn_k.weight", "attn_v.weight"))
-        self.w_gu = stack(("ffn_gate.weight", "ffn_up.weight"))
         self.w_o = ops.Q8Matrix(*split["attn_output.weight"], hid, H * d)
         self.w_down = ops.Q8Matrix(*split["ffn_down.weight"], hid, ffn)
         self.w_q = _Rows(self.w_qkv, 0, H * d)
         self.w_k = _Rows(self.w_qkv, H * d, Hkv * d)
         self.w_v = _Rows(self.w_qkv, (H + Hkv) * d, Hkv * d)
-        self.w_gate = _Rows(self.w_gu, 0, ffn)
-        self.w_up = _Rows(self.w_gu, ffn, ffn)
+        # gate and up: rows interleaved (gate_i, up_i), so one projection also
+        # applies SwiGLU (flk_q8_gate_up_swiglu, hidden <= 1024); else stacked
+        # and SwiGLU rides in the down projection's input.
+        self.paired = hid <= 1024
+        if self.paired:
+            g_qs, g_sc = split["ffn_gate.weight"]
+            u_qs, u_sc = split["ffn_up.weight"]
+            self.w_gu = ops.Q8Matrix(ops.interleave_rows(g_qs, u_qs, ffn, hid),
+                                     ops.interleave_rows(g_sc, u_sc, ffn, hid // 32), 2 * ffn, hid)
+        else:
+            self.w_gu = stack(("ffn_gate.weight", "ffn_up.weight"))
+            self.w_gate = _Rows(self.w_gu, 0, ffn)
+            self.w_up = _Rows(self.w_gu, ffn, ffn)
         self.g = {}
         for name in GAINS:
             want = d if "q_norm" in name or "k_norm" in name else hid
@@ -123,9 +136,11 @@ class DecoderLayer:
             "q": B(P * H * d * f), "k": B(P * Hkv * d * f), "v": B(P * Hkv * d * f),
             "qn": B(P * H * d * f), "attn": B(P * H * d * f),
             "gu": B(2 * ffn * f), "gate": B(P * ffn * f), "up": B(P * ffn * f),
+            "act": B(P * ffn * f),
             "kcache": B(cfg.maxKeys * Hkv * d * f), "vcache": B(cfg.maxKeys * Hkv * d * f),
             "invFreq": B.from_array(ops.rope_inv_freq(d, cfg.ropeBase)),
         }
+        self.out_dev = B(hid * f)
         self.ws = ops.Workspace(H, Hkv, d, cfg.maxKeys, P, 1)
         self.nKeys = 0
 
@@ -171,16 +186,53 @@ class DecoderLayer:
                          b["qn"], b["kcache"], b["vcache"], b["attn"], pos, H, Hkv, d,
                          cfg.maxKeys, self.ws)
         ops.q8_matvec_ex(self.w_o, b["attn"], b["h2"], 1, res=hin)
-        ops.q8_matvec_ex(self.w_gu, b["h2"], b["gu"], 1, norm_gain=g["ffn_norm.weight"],
-                         eps=cfg.eps)
-        ops.q8_matvec_ex(self.w_down, b["gu"], b["out"], 1, up=b["gu"].ptr + cfg.ffn * 4,
-                         res=b["h2"])
+        self._ffn(1, b["out"])
         self._chain()
         self.nKeys = pos + 1
 
+    def _ffn(self, n: int, out) -> None:
+        """out = h2 + W_down swiglu(W_gate nh2, W_up nh2), nh2 = rmsnorm(h2)."""
+        cfg, b, g = self.cfg, self.buf, self.g
+        if self.paired:
+            ops.q8_gate_up_swiglu(self.w_gu, b["h2"], b["act"], n, norm_gain=g["ffn_norm.weight"],
+                                  eps=cfg.eps)
+            ops.q8_matvec_ex(self.w_down, b["act"], out, n, res=b["h2"])
+        elif n == 1:
+            ops.q8_matvec_ex(self.w_gu, b["h2"], b["gu"], 1, norm_gain=g["ffn_norm.weight"],
+                             eps=cfg.eps)
+            ops.q8_matvec_ex(self.w_down, b["gu"], out, 1, up=b["gu"].ptr + cfg.ffn * 4,
+                             res=b["h2"])
+        else:
+            for w, o in ((self.w_gate, b["gate"]), (self.w_up, b["up"])):
+                ops.q8_matvec_ex(w, b["h2"], o, n, norm_gain=g["ffn_norm.weight"], eps=cfg.eps)
+            ops.q8_matvec_ex(self.w_down, b["gate"], out, n, up=b["up"], res=b["h2"])
+
+    def encode_dev(self, src, n_keys_dev) -> None:
+        """One decode step whose position lives in device memory
+        (*n_keys_dev = position + 1): the form a captured, replayed step uses.
+        Reads its input from ``src`` and writes ``outputBufferDev()``; no host
+        bookkeeping (the caller tracks the position and the cache bound)."""
+        cfg, b, g = self.cfg, self.buf, self.g
+        H, Hkv, d = cfg.nHeads, cfg.nKvHeads, cfg.headDim
+        qkv = b["qkv"].ptr
+        ops.q8_matvec_ex(self.w_qkv, src, b["qkv"], 1, norm_gain=g["attn_norm.weight"],
+                         eps=cfg.eps)
+        ops.decode_layer_dev(qkv, qkv + H * d * 4, qkv + (H + Hkv) * d * 4,
+                             g["attn_q_norm.weight"], g["attn_k_norm.weight"], b["invFreq"],
+                             cfg.eps, cfg.ropePairing, b["qn"], b["kcache"], b["vcache"],
+                             b["attn"], n_keys_dev, H, Hkv, d, cfg.maxKeys, self.ws)
+        ops.q8_matvec_ex(self.w_o, b["attn"], b["h2"], 1, res=src)
+        self._ffn(1, self.out_dev)
+
+    def outputBufferDev(self) -> ops.DeviceBuffer:
+        """Where encode_dev writes (fixed, so a captured step can chain layers)."""
+        return self.out_dev
+
     # ----------------------------------------------------------------- prefill
-    def encodePrefill(self, nTokens: int, hidden=None, offset: int | None = None) -> None:
-        """nTokens positions starting at nKeys (layer.ts:685-767)."""
+    def encodePrefill(self, nTokens: int, hidden=None, offset: int | None = None,
+                      src=None) -> None:
+        """nTokens positions starting at nKeys (layer.ts:685-767); ``src``: read
+        the input rows from that device buffer (no copy)."""
         cfg, b, g = self.cfg, self.buf, self.g
         H, Hkv, d, hid, ffn = cfg.nHeads, cfg.nKvHeads, cfg.headDim, cfg.hidden, cfg.ffn
         pos = self.nKeys
@@ -193,16 +245,15 @@ class DecoderLayer:
             raise CacheFullError(-2, f"KV cache would exceed {cfg.maxKeys} keys ({pos} + {nTokens})")
         self._hidden_in(nTokens, hidden)
         n = nTokens
+        hin = b["h"] if src is None else src
         for w, out in ((self.w_q, b["q"]), (self.w_k, b["k"]), (self.w_v, b["v"])):
-            ops.q8_matvec_ex(w, b["h"], out, n, norm_gain=g["attn_norm.weight"], eps=cfg.eps)
+            ops.q8_matvec_ex(w, hin, out, n, norm_gain=g["attn_norm.weight"], eps=cfg.eps)
         ops.qk_prologue(b["q"], b["k"], b["v"], g["attn_q_norm.weight"], g["attn_k_norm.weight"],
                         b["invFreq"], cfg.eps, cfg.ropePairing, b["qn"], b["kcache"],
                         b["vcache"], n, pos, H, Hkv, d, cfg.maxKeys)
         ops.attn_prefill(b["qn"], b["kcache"], b["vcache"], b["attn"], H, Hkv, d, n, pos, self.ws)
-        ops.q8_matvec_ex(self.w_o, b["attn"], b["h2"], n, res=b["h"])
-        for w, out in ((self.w_gate, b["gate"]), (self.w_up, b["up"])):
-            ops.q8_matvec_ex(w, b["h2"], out, n, norm_gain=g["ffn_norm.weight"], eps=cfg.eps)
-        ops.q8_matvec_ex(self.w_down, b["gate"], b["out"], n, up=b["up"], res=b["h2"])
+        ops.q8_matvec_ex(self.w_o, b["attn"], b["h2"], n, res=hin)
+        self._ffn(n, b["out"])
         self._chain()
         self.nKeys = pos + n
 
@@ -229,6 +280,6 @@ class DecoderLayer:
         for m in (self.w_qkv, self.w_gu, self.w_o, self.w_down):
             m.qs.free()
             m.scales.free()
-        for x in list(self.buf.values()) + list(self.g.values()):
+        for x in list(self.buf.values()) + list(self.g.values()) + [self.out_dev]:
             x.free()
         self.ws.free()

@@ -111,6 +111,8 @@ def set_stream(stream) -> None:
         h = None
     elif isinstance(stream, int):
         h = stream
+    elif isinstance(stream, Stream):
+        h = stream.handle
     else:
         h = int(stream.cuda_stream)
     check(lib().flk_set_stream(h), "flk_set_stream")
@@ -190,6 +192,18 @@ def decode_layer(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps: float, pairing, qn_
                                  max_keys, w, nb), "flk_decode_layer")
 
 
+def decode_layer_dev(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps: float, pairing, qn_out, kcache,
+                     vcache, o, n_keys_dev, n_heads: int, n_kv_heads: int, head_dim: int,
+                     max_keys: int, ws) -> None:
+    """flk_decode_layer with the key count (position + 1) in device memory."""
+    w, nb = _ws(ws)
+    check(lib().flk_decode_layer_dev(ptr(q_raw), ptr(k_raw), ptr(v_raw), ptr(gq), ptr(gk),
+                                     ptr(inv_freq), eps, _pairing(pairing), ptr(qn_out),
+                                     ptr(kcache), ptr(vcache), ptr(o), ptr(n_keys_dev), n_heads,
+                                     n_kv_heads, head_dim, max_keys, w, nb),
+          "flk_decode_layer_dev")
+
+
 def attn_decode_ragged(q, kcache, vcache, seq_row_off, n_keys, o, n_seqs: int, max_n_keys: int,
                        n_heads: int, n_kv_heads: int, head_dim: int, ws) -> None:
     w, nb = _ws(ws)
@@ -247,6 +261,21 @@ def q8_matvec_ex(w: "Q8Matrix", x, o, n_tokens: int = 1, norm_gain=None, eps: fl
           "flk_q8_matvec_ex")
 
 
+def q8_gate_up_swiglu(w: "Q8Matrix", x, act, n_tokens: int = 1, norm_gain=None,
+                      eps: float = 0.0) -> None:
+    """act = swiglu(gate, up) of the (gate, up)-interleaved matrix ``w`` times f(x)."""
+    check(lib().flk_q8_gate_up_swiglu(ptr(w.qs), ptr(w.scales), ptr(x), ptr(act), w.rows // 2,
+                                      w.cols, n_tokens, ptr(norm_gain), eps),
+          "flk_q8_gate_up_swiglu")
+
+
+def interleave_rows(a, b, rows: int, row_len: int) -> np.ndarray:
+    """Rows a0, b0, a1, b1, ... of two [rows][row_len] arrays."""
+    a = np.asarray(a).reshape(rows, row_len)
+    b = np.asarray(b).reshape(rows, row_len)
+    return np.stack([a, b], axis=1).reshape(-1)
+
+
 def swiglu(gate, up, o, n: int) -> None:
     """elementwise.wgsl swiglu: o = silu(gate) * up."""
     check(lib().flk_swiglu(ptr(gate), ptr(up), ptr(o), n), "flk_swiglu")
@@ -281,3 +310,70 @@ def lm_head(x, gain, eps: float, w: "Q8Matrix", normed, logits, oval, oidx, ws) 
     check(lib().flk_lm_head(ptr(x), ptr(gain), eps, ptr(w.qs), ptr(w.scales), w.rows, w.cols,
                             ptr(normed), ptr(logits), ptr(oval), ptr(oidx), wsp, nb),
           "flk_lm_head")
+
+
+
+# ------------------------------------------------------------- graphs
+def embed(w: "Q8Matrix", ids, n_tokens: int, out) -> None:
+    """embed.wgsl: out[t] = dequantized row ids[t] of ``w`` (device ids)."""
+    check(lib().flk_embed(ptr(w.qs), ptr(w.scales), ptr(ids), n_tokens, w.rows, w.cols, ptr(out)),
+          "flk_embed")
+
+
+def advance(state, delta: int = 1, value=None, log=None, log_len: int = 0) -> None:
+    """state = device {n_keys, cursor}: n_keys += delta; log[cursor++] = *value."""
+    check(lib().flk_advance(ptr(state), delta, ptr(value), ptr(log), log_len), "flk_advance")
+
+
+class Stream:
+    """A library-created stream of default priority (capturable)."""
+
+    def __init__(self):
+        h = ctypes.c_void_p()
+        check(lib().flk_stream_create(ctypes.byref(h)), "flk_stream_create")
+        self.handle = h.value
+
+    def free(self) -> None:
+        if self.handle:
+            lib().flk_stream_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass
+
+
+class Graph:
+    """Calls made inside ``with Graph() as g:`` are captured from the library
+    stream (not run); ``g.launch()`` replays them."""
+
+    def __init__(self):
+        self.handle = None
+
+    def __enter__(self):
+        check(lib().flk_capture_begin(), "flk_capture_begin")
+        return self
+
+    def __exit__(self, exc_type, exc, tb):
+        h = ctypes.c_void_p()
+        rc = lib().flk_capture_end(ctypes.byref(h))
+        if exc_type is None:
+            check(rc, "flk_capture_end")
+        self.handle = h.value
+        return False
+
+    def launch(self) -> None:
+        check(lib().flk_graph_launch(self.handle), "flk_graph_launch")
+
+    def free(self) -> None:
+        if self.handle:
+            lib().flk_graph_destroy(self.handle)
+            self.handle = None
+
+    def __del__(self):
+        try:
+            self.free()
+        except Exception:
+            pass

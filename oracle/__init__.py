@@ -396,3 +396,16 @@ def wire_unpack(buf: bytes):
     data = np.array([f16_to_f32_wire(int(h)) for h in hs], np.float32)
     return data, dict(seq=seq, hidden=hidden, offset=offset, reset=bool(flags & 1),
                       replay=bool(flags & 2))
+
+
+def embed(packed, ids, vocab: int, hidden: int) -> np.ndarray:
+    """embed.wgsl (kernels/embed.wgsl:52-75): row ids[t] of a Q8_0 matrix,
+    each element the f32 product q * scale (scale per halfToF32)."""
+    qs, sc = split_q8(packed, vocab, hidden)
+    ids = np.asarray(ids, np.int64).ravel()
+    out = np.empty((ids.size, hidden), np.float32)
+    nb = hidden // 32
+    for t, r in enumerate(ids):
+        s = np.array([half_to_f32(int(h)) for h in sc[r * nb:(r + 1) * nb]], np.float32)
+        out[t] = qs[r * hidden:(r + 1) * hidden].astype(np.float32) * np.repeat(s, 32)
+    return out.ravel()

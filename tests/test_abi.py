@@ -19,7 +19,7 @@ from flock_amd import _lib
 
 ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
 HEADERS = [os.path.join(ROOT, "include", h) for h in ("flock_attn.h", "flock_q8.h",
-                                                      "flock_wire.h")]
+                                                      "flock_wire.h", "flock_graph.h")]
 FAKE = 0x1000  # never dereferenced: every call below fails validation first
 
 

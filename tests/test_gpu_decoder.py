@@ -152,3 +152,34 @@ def test_guards(rng):
     with pytest.raises(Exception, match="KV cache full at 2 keys"):
         layer.encode(x)
     layer.free()
+
+
+@pytest.mark.parametrize("ffn,hid,n", [(3072, 1024, 1), (3072, 1024, 3), (500, 256, 2), (64, 64, 1)])
+def test_gate_up_swiglu_matches_separate_ops(rng, ffn, hid, n):
+    gate = random_packed(rng, ffn, hid)
+    up = random_packed(rng, ffn, hid)
+    gq, gs = ops.q8_split(gate, ffn, hid)
+    uq, us = ops.q8_split(up, ffn, hid)
+    w = ops.Q8Matrix(ops.interleave_rows(gq, uq, ffn, hid),
+                     ops.interleave_rows(gs, us, ffn, hid // 32), 2 * ffn, hid)
+    x = rng.standard_normal(n * hid).astype(np.float32) * 2
+    gain = rng.normal(1, 0.1, hid).astype(np.float32)
+    act = ops.DeviceBuffer(n * ffn * 4)
+    ops.q8_gate_up_swiglu(w, dev(x), act, n, norm_gain=dev(gain), eps=EPS)
+    ops.sync()
+    nx = oracle.rmsnorm(x, gain, hid, n, EPS)
+    want = oracle.swiglu(oracle.q8_matvec(gate, nx, ffn, hid, 64, fused=True),
+                         oracle.q8_matvec(up, nx, ffn, hid, 64, fused=True))
+    assert np.array_equal(act.download(n * ffn), want)
+    # Without the norm.
+    ops.q8_gate_up_swiglu(w, dev(x), act, n)
+    ops.sync()
+    want = oracle.swiglu(oracle.q8_matvec(gate, x, ffn, hid, 64, fused=True),
+                         oracle.q8_matvec(up, x, ffn, hid, 64, fused=True))
+    assert np.array_equal(act.download(n * ffn), want)
+
+
+def test_gate_up_swiglu_rejects_wide_rows():
+    from flock_amd import _lib
+    rc = _lib.lib().flk_q8_gate_up_swiglu(0x1000, 0x1000, 0x1000, 0x1000, 8, 2048, 1, None, 0.0)
+    assert rc == _lib.FLK_ERR_UNSUPPORTED
