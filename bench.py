@@ -36,7 +36,8 @@ of the hot path over one batch of synthetic, HBM-resident input:
   gen512     The same from position 512.
 
 The default run also measures prefill2k (the metric's second half) and reports
-it under "prefill", and the LM-head projection under "q8_lm_head". Inputs are N(0, 1) from a seeded generator (gains
+it under "prefill", the LM-head projection under "q8_lm_head", and whole-model
+greedy generation at 32k context (gen32k) under "generate". Inputs are N(0, 1) from a seeded generator (gains
 N(1, 0.1)); caches are written on the device before timing starts.
 
 Timing: HIP events recorded on the stream the kernels are launched on bracket
@@ -698,7 +699,7 @@ def main():
     ap.add_argument("--workload", default="decode32k", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
-                    help="skip the prefill2k and q8lmhead measurements of the default run")
+                    help="skip the prefill2k, q8lmhead and gen32k measurements of the default run")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -739,6 +740,9 @@ def main():
             q, q8_cpu = run(torch, ops, stream, "q8lmhead", max(5, args.steps), args.warmup)
             q["frac_of_hbm_peak"] = round(q["value"] / HBM_PEAK_GBS, 4)
             out["q8_lm_head"] = q
+            g, _ = run(torch, ops, stream, "gen32k", 5, 2)
+            g["frac_of_hbm_peak"] = round(g["value"] / HBM_PEAK_GBS, 4)
+            out["generate"] = g
     # CPU baselines last, with the GPU measurements done.
     if not args.no_cpu_baseline:
         log(f"[{args.workload}] CPU baseline (oracle port, 1 thread)")
