@@ -34,11 +34,17 @@ of the hot path over one batch of synthetic, HBM-resident input:
              (flock_amd.model): 32 tokens per step from position 32768.
              GB/s and tokens/s.
   gen512     The same from position 512.
+  q8prefill  The largest prefill projection: ffn_norm + gate/up (2 x 3072 x
+             1024) + SwiGLU over 2048 tokens in one call (the weight-reusing
+             tile kernel). TFLOP/s against the fp32 vector peak.
+  prompt2k   Time to first token: a 2048-token prompt through Model.step
+             (28 layers in prefill + head). tokens/s and ms per prompt.
 
 The default run also measures prefill2k (the metric's second half) and reports
-it under "prefill", the LM-head projection under "q8_lm_head", and whole-model
-greedy generation at 32k context (gen32k) under "generate". Inputs are N(0, 1) from a seeded generator (gains
-N(1, 0.1)); caches are written on the device before timing starts.
+it under "prefill", the LM-head projection under "q8_lm_head", whole-model
+greedy generation at 32k context (gen32k) under "generate" and the 2048-token
+prompt (prompt2k) under "prompt". Inputs are N(0, 1) from a seeded generator
+(gains N(1, 0.1)); caches are written on the device before timing starts.
 
 Timing: HIP events recorded on the stream the kernels are launched on bracket
 the K timed steps (after a synchronize). The roofline's average call duration
@@ -64,6 +70,9 @@ sys.path.insert(0, ROOT)
 METRIC = "decode-attn HBM GB/s (% peak) @32k ctx; prefill-attn TFLOP/s (% MFMA peak) @2k"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
+# MI355X published fp32 vector peak. It counts packed-fp32 instructions, which
+# this library never emits, so 78.6 TFLOP/s is the ceiling its VALU code can reach.
+FP32_VECTOR_PEAK_TFLOPS = 157.3
 H, HKV, D = 16, 8, 128
 EPS = 9.999999974752427e-7
 PROFILES = os.path.join(ROOT, "profiles")
@@ -105,6 +114,9 @@ class Workload:
         if self.bound == "hbm":
             achieved = self.work_per_call / (call_ms * 1e-3) / 1e9
             peak, unit, key = HBM_PEAK_GBS, "GB/s", "bytes_per_launch"
+        elif self.bound == "valu":
+            achieved = self.work_per_call / (call_ms * 1e-3) / 1e12
+            peak, unit, key = FP32_VECTOR_PEAK_TFLOPS, "TFLOP/s", "flops_per_launch"
         else:
             achieved = self.work_per_call / (call_ms * 1e-3) / 1e12
             peak, unit, key = FP32_MFMA_PEAK_TFLOPS, "TFLOP/s", "flops_per_launch"
@@ -466,6 +478,114 @@ class Q8Proj(Workload):
                     r * c * 34 // 32 for r, c in self.shapes)}
 
 
+def random_q8(rng, rows, cols, scale=8e-4):
+    """Q8_0 bytes (34-byte blocks) with random quants and f16 scales."""
+    blocks = np.empty((rows * cols // 32, 34), np.uint8)
+    blocks[:, :2] = (rng.random(blocks.shape[0]) * scale + 1e-5).astype(
+        np.float16).view(np.uint8).reshape(-1, 2)
+    blocks[:, 2:] = rng.integers(0, 256, (blocks.shape[0], 32), dtype=np.uint8)
+    return blocks.ravel()
+
+
+class Q8Prefill(Workload):
+    """The largest projection of a 2048-token prefill: ffn_norm, then gate and
+    up (3072 x 1024 each, rows interleaved) with SwiGLU, in one
+    flk_q8_gate_up_swiglu call over 2048 tokens -- the weight-reusing tile
+    kernel (q8_mm_kernel), exact to the coop(64) order. VALU-bound: the
+    exact summation order rules out MFMA."""
+
+    name = "q8prefill"
+    unit = "TFLOP/s"
+    bound = "valu"
+    kernel = "flk_q8_gate_up_swiglu: q8_mm_kernel<true,false> (32 rows x 8 tokens per workgroup)"
+    n_tokens, ffn, hid = 2048, 3072, 1024
+
+    def __init__(self, torch, ops):
+        self.torch, self.ops = torch, ops
+        rng = np.random.default_rng(29)
+        gq, gs = ops.q8_split(random_q8(rng, self.ffn, self.hid), self.ffn, self.hid)
+        uq, us = ops.q8_split(random_q8(rng, self.ffn, self.hid), self.ffn, self.hid)
+        self.w = ops.Q8Matrix(ops.interleave_rows(gq, uq, self.ffn, self.hid),
+                              ops.interleave_rows(gs, us, self.ffn, self.hid // 32),
+                              2 * self.ffn, self.hid)
+        self.x = ops.DeviceBuffer.from_array(
+            rng.standard_normal(self.n_tokens * self.hid).astype(np.float32))
+        self.gain = ops.DeviceBuffer.from_array((1 + 0.1 * rng.standard_normal(self.hid)).astype(np.float32))
+        self.act = ops.DeviceBuffer(self.n_tokens * self.ffn * 4)
+        self.work_per_call = 2 * (2 * self.ffn) * self.hid * self.n_tokens  # 2 flops per MAC
+        self.work_per_step = self.work_per_call
+
+    def call(self, i=0):
+        self.ops.q8_gate_up_swiglu(self.w, self.x, self.act, self.n_tokens, norm_gain=self.gain,
+                                   eps=EPS)
+
+    def step(self):
+        self.call()
+
+    def config(self):
+        return {"workload": "Q8_0 gate+up (2 x 3072 x 1024, interleaved) with ffn_norm in and "
+                            "SwiGLU out, 2048 tokens", "rows": 2 * self.ffn, "cols": self.hid,
+                "tokens": self.n_tokens}
+
+
+class Prompt2k(Workload):
+    """Time to first token: a 2048-token prompt through flock_amd.model.Model.step
+    (embedding, 28 Qwen3-0.6B layers in prefill -- Q8_0 tile projections with
+    fused norms and SwiGLU, q/k norm + RoPE + K/V write, fp32-MFMA causal
+    attention -- then the head and argmax on the last row, read back)."""
+
+    name = "prompt2k"
+    unit = "tokens/s"
+    bound = "valu"
+    kernel = "Model.step(2048 ids): embed, 28 x encodePrefill, lm_head"
+    n_tokens = 2048
+
+    def __init__(self, torch, ops):
+        from flock_amd.decoder import DecoderConfig
+        from flock_amd.model import Model
+        self.torch, self.ops = torch, ops
+        rng = np.random.default_rng(30)
+        cfg = DecoderConfig(maxKeys=self.n_tokens, maxPrefill=self.n_tokens)
+        log(f"[{self.name}] building the model (random Q8_0 weights)")
+        layers = []
+        for _ in range(28):
+            w = {n: random_q8(rng, r, c) for n, (r, c) in cfg.shapes().items()}
+            for n, sz in (("attn_norm.weight", cfg.hidden), ("ffn_norm.weight", cfg.hidden),
+                          ("attn_q_norm.weight", cfg.headDim), ("attn_k_norm.weight", cfg.headDim)):
+                w[n] = (1 + 0.1 * rng.standard_normal(sz)).astype(np.float32)
+            layers.append(w)
+        self.vocab = 151936
+        self.model = Model(cfg, layers, random_q8(rng, self.vocab, cfg.hidden, 0.02),
+                           (1 + 0.1 * rng.standard_normal(cfg.hidden)).astype(np.float32),
+                           self.vocab, max_generate=1)
+        del layers
+        self.ids = rng.integers(0, self.vocab, self.n_tokens).astype(np.uint32)
+        macs = sum(r * c for r, c in cfg.shapes().values())
+        n, H, d = self.n_tokens, cfg.nHeads, cfg.headDim
+        attn = 4 * H * d * n * (n + 1) // 2  # QK^T and PV over the causal triangle
+        self.work_per_call = 28 * (2 * macs * n + attn) + 2 * self.vocab * cfg.hidden
+        self.work_per_step = self.work_per_call
+
+    def value(self, ms):
+        return self.n_tokens / (ms * 1e-3)
+
+    def call(self, i=0):
+        self.model.reset()
+        self.model.step(self.ids)
+
+    def step(self):
+        self.call()
+
+    def extra(self, ms):
+        return {"ms_per_prompt": round(ms, 3)}
+
+    def config(self):
+        return {"workload": "time to first token: 2048-token prompt at position 0 through 28 "
+                            "Qwen3-0.6B layers (prefill) + output norm + LM head + argmax",
+                "layers": 28, "tokens": self.n_tokens, "vocab": self.vocab,
+                "flops_per_prompt": self.work_per_call}
+
+
 class Token(Workload):
     """One greedy decode token through all 28 Qwen3-0.6B layers and the head:
     per layer the five DecoderLayer calls (fused projections + the attention
@@ -625,7 +745,8 @@ class Gen512(Gen):
 
 
 WORKLOADS = {c.name: c for c in (Decode32k, Prefill2k, Ragged, Chunk32k, Decode512, Copy,
-                                 Q8LmHead, Q8Proj, Token32k, Token512, Gen32k, Gen512)}
+                                 Q8LmHead, Q8Proj, Q8Prefill, Prompt2k, Token32k, Token512,
+                                 Gen32k, Gen512)}
 
 
 def settle_clocks(torch, w, seconds=0.5):
@@ -699,7 +820,8 @@ def main():
     ap.add_argument("--workload", default="decode32k", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
-                    help="skip the prefill2k, q8lmhead and gen32k measurements of the default run")
+                    help="skip the prefill2k, q8lmhead, gen32k and prompt2k measurements of the "
+                         "default run")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -730,8 +852,12 @@ def main():
                 out[k] = main_res[k]
         if main_res["unit"] == "GB/s":
             out["frac_of_hbm_peak"] = round(main_res["value"] / HBM_PEAK_GBS, 4)
-        else:
+        elif main_res["unit"] == "TFLOP/s" and main_res["roofline"]["bound"] == "mfma":
             out["frac_of_fp32_mfma_peak"] = round(main_res["value"] / FP32_MFMA_PEAK_TFLOPS, 4)
+        elif main_res["unit"] == "TFLOP/s":
+            out["frac_of_fp32_vector_peak"] = round(main_res["value"] / FP32_VECTOR_PEAK_TFLOPS, 4)
+        if "ms_per_prompt" in main_res:
+            out["ms_per_prompt"] = main_res["ms_per_prompt"]
         pre_cpu = q8_cpu = None
         if args.workload == "decode32k" and not args.no_secondary:
             p, pre_cpu = run(torch, ops, stream, "prefill2k", max(5, args.steps), args.warmup)
@@ -743,6 +869,8 @@ def main():
             g, _ = run(torch, ops, stream, "gen32k", 5, 2)
             g["frac_of_hbm_peak"] = round(g["value"] / HBM_PEAK_GBS, 4)
             out["generate"] = g
+            t, _ = run(torch, ops, stream, "prompt2k", 3, 1)
+            out["prompt"] = t
     # CPU baselines last, with the GPU measurements done.
     if not args.no_cpu_baseline:
         log(f"[{args.workload}] CPU baseline (oracle port, 1 thread)")

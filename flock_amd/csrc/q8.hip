@@ -34,6 +34,13 @@ constexpr int kQ8Threads = 256;   // 4 waves
 #ifndef FLK_Q8_WG_PER_CU
 #define FLK_Q8_WG_PER_CU 0  // 0: as many as fit (occupancy query)
 #endif
+// Batches of at least this many tokens take the weight-reusing tile kernel.
+#ifndef FLK_Q8_MM_MIN_TOKENS
+#define FLK_Q8_MM_MIN_TOKENS 8
+#endif
+#ifndef FLK_Q8_MM_WAVES
+#define FLK_Q8_MM_WAVES 2  // waves per SIMD the tile kernel is register-limited to
+#endif
 template <int NB>
 constexpr int q8_unroll() { return NB == 1 ? FLK_Q8_UNROLL : (NB == 2 ? 2 : 1); }
 constexpr int kQ8MaxRegBlocks = 4;  // x blocks per lane kept in registers (8192 columns)
@@ -325,6 +332,240 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
   if (a.best_val != nullptr) argmax_block_store(bv, bi, a.best_val, a.best_idx);
 }
 
+// ---------------------------------------------------------------------------
+// Many tokens at once (prefill, replay chunks): the same sums, with every
+// weight block used for several tokens instead of re-read per token.
+//
+// A workgroup owns a tile of kMmRows rows x kMmTokens tokens. Each output
+// keeps the coop(64) order: 32 physical lanes q hold leaf q (blocks q, q + 64,
+// ...) and, when the row has more than 32 blocks, leaf q + 32 (blocks q + 32,
+// q + 96, ...) in a second accumulator; their sum is the tree's stride-32
+// step, and strides 16 .. 1 run across the 32 lanes. A lane holds
+// kMmRowsPerSlot x kMmTokens outputs, so the cross-lane strides use recursive
+// halving (each exchange moves half of the lane's values: 31 exchanges for 32
+// outputs instead of 5 per output) -- the same pairs are added, only which
+// lane keeps which sum differs, and f32 addition is commutative.
+//
+// x is staged through LDS in chunks of 32 blocks (1024 columns) with any input
+// fusion applied there; each lane reads its block of every token (blocks
+// padded to 36 floats so the 16 lanes of a read phase hit distinct banks).
+// Weights come straight from memory, requested before the staging barrier.
+constexpr int kMmRowsPerSlot = 4;
+constexpr int kMmTokens = 8;
+constexpr int kMmRows = (kQ8Threads / kWave) * 2 * kMmRowsPerSlot;  // 32
+constexpr int kMmPad = 36;
+constexpr int kMmChunkCols = 1024;
+constexpr int kMmTokenStride = 32 * kMmPad;  // floats per staged token
+
+// One block of RT rows (weights w0/w1, scales sc) against the staged tokens,
+// folded into acc[r][t] (q8_coop.wgsl:105-112 per output).
+template <int RT, int TT>
+__device__ __forceinline__ void q8_mm_block(float (&acc)[RT][TT], const uint4 (&w0)[RT],
+                                            const uint4 (&w1)[RT], const float (&sc)[RT],
+                                            const float* xb) {
+#pragma unroll
+  for (int g = 0; g < 4; g++) {
+    float qf[RT][8];
+#pragma unroll
+    for (int r = 0; r < RT; r++) {
+      const uint32_t wa = g == 0 ? w0[r].x : g == 1 ? w0[r].z : g == 2 ? w1[r].x : w1[r].z;
+      const uint32_t wb = g == 0 ? w0[r].y : g == 1 ? w0[r].w : g == 2 ? w1[r].y : w1[r].w;
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        qf[r][k] = q8_quant(wa, k);
+        qf[r][4 + k] = q8_quant(wb, k);
+      }
+    }
+#pragma unroll
+    for (int t = 0; t < TT; t++) {
+      const float4 xa = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g);
+      const float4 xc = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g + 4);
+#pragma unroll
+      for (int r = 0; r < RT; r++) {
+        float d0 = qf[r][0] * xa.x;
+        d0 = __builtin_fmaf(qf[r][1], xa.y, d0);
+        d0 = __builtin_fmaf(qf[r][2], xa.z, d0);
+        d0 = __builtin_fmaf(qf[r][3], xa.w, d0);
+        float d1 = qf[r][4] * xc.x;
+        d1 = __builtin_fmaf(qf[r][5], xc.y, d1);
+        d1 = __builtin_fmaf(qf[r][6], xc.z, d1);
+        d1 = __builtin_fmaf(qf[r][7], xc.w, d1);
+        acc[r][t] = __builtin_fmaf(sc[r], d0 + d1, acc[r][t]);
+      }
+    }
+  }
+}
+
+// Tile (row tile, token tile) of workgroup `id`. When the row tiles split
+// evenly over the 8 XCDs (workgroups go to XCDs round-robin by id), XCD x
+// takes a contiguous eighth of the rows and walks it token tile by token
+// tile, so its share of the weights stays in its own L2 while x streams.
+__device__ __forceinline__ void q8_mm_tile(uint32_t id, uint32_t n_rt, uint32_t& rt,
+                                           uint32_t& tt) {
+  if (n_rt % 8 == 0) {
+    const uint32_t per = n_rt / 8, k = id / 8;
+    rt = (id % 8) * per + k % per;
+    tt = k / per;
+  } else {
+    rt = id % n_rt;
+    tt = id / n_rt;
+  }
+}
+
+// Chunk c (blocks 32c .. 32c + 31) of a tile: lane q's weights for block
+// 32c + q are requested, x's columns 1024c .. 1024c + 1023 of the tile's tokens
+// are staged (with the input fusion), and the block is folded into acc.
+template <bool FUSE, int RT, int TT>
+__device__ __forceinline__ void q8_mm_chunk(const Q8Args& a, uint32_t c, int q, uint32_t tok0,
+                                            const uint8_t* const (&wrow)[RT],
+                                            const uint16_t* const (&srow)[RT], float* xs,
+                                            const float* s_scale, float (&acc)[RT][TT]) {
+  const uint32_t nb = a.n_cols / 32;
+  const uint32_t b = 32 * c + q;
+  const uint32_t bl = min(b, nb - 1);
+  uint4 w0[RT], w1[RT];
+  float sc[RT];
+#pragma unroll
+  for (int r = 0; r < RT; r++) {
+    const uint4* src = reinterpret_cast<const uint4*>(wrow[r] + 32 * (size_t)bl);
+    w0[r] = src[0];
+    w1[r] = src[1];
+    sc[r] = q8_scale(srow[r][bl]);
+  }
+  __syncthreads();  // the previous chunk's reads are done (and s_scale is visible)
+  // TT tokens x 256 float4s, 8 per thread.
+#pragma unroll
+  for (int k = 0; k < TT * (kMmChunkCols / 4) / kQ8Threads; k++) {
+    const uint32_t f = threadIdx.x + kQ8Threads * k;
+    const uint32_t t = f / (kMmChunkCols / 4), j = f % (kMmChunkCols / 4);
+    const uint32_t col = kMmChunkCols * c + 4 * j;
+    if (col >= a.n_cols) continue;
+    const uint32_t tok = min(tok0 + t, a.n_tokens - 1);
+    const size_t off = (size_t)tok * a.n_cols + col;
+    float4 v = *reinterpret_cast<const float4*>(a.x + off);
+    if (FUSE) {
+      if (a.norm_gain != nullptr) {
+        const float s = s_scale[t];
+        const float4 gn = *reinterpret_cast<const float4*>(a.norm_gain + col);
+        v = make_float4((v.x * s) * gn.x, (v.y * s) * gn.y, (v.z * s) * gn.z, (v.w * s) * gn.w);
+      } else {
+        const float4 u = *reinterpret_cast<const float4*>(a.up + off);
+        v = make_float4(q8_swiglu(v.x, u.x), q8_swiglu(v.y, u.y), q8_swiglu(v.z, u.z),
+                        q8_swiglu(v.w, u.w));
+      }
+    }
+    *reinterpret_cast<float4*>(xs + t * kMmTokenStride + (j / 8) * kMmPad + 4 * (j % 8)) = v;
+  }
+  __syncthreads();
+  if (b < nb) q8_mm_block<RT, TT>(acc, w0, w1, sc, xs + q * kMmPad);
+}
+
+// One recursive-halving step over v[0 .. N): lanes with bit S clear keep
+// v[0 .. N/2), the others v[N/2 .. N) moved down; each adds its partner's
+// copy. Written with constant indices only (a select between two array
+// elements would otherwise become a select of the index and a scan of the
+// whole array).
+template <int S, int N, int I = 0>
+__device__ __forceinline__ void q8_halve_step(float (&v)[32], bool hi) {
+  if constexpr (I < N / 2) {
+    const float lo = v[I], up = v[I + N / 2];
+    v[I] = (hi ? up : lo) + shfl_xor(hi ? lo : up, S);
+    q8_halve_step<S, N, I + 1>(v, hi);
+  }
+}
+template <int S, int N>
+__device__ __forceinline__ void q8_halve(float (&v)[32], int q) {
+  if constexpr (S >= 1) {
+    q8_halve_step<S, N>(v, (q & S) != 0);
+    q8_halve<S / 2, N / 2>(v, q);
+  }
+}
+
+// TWO: the rows have more than 32 blocks (leaf q + 32 exists).
+template <bool FUSE, bool TWO>
+__global__ __launch_bounds__(kQ8Threads, TWO ? FLK_Q8_MM_WAVES : FLK_Q8_MM_WAVES + 1) void q8_mm_kernel(Q8Args a, uint32_t n_rt) {
+  constexpr int RT = kMmRowsPerSlot, TT = kMmTokens;
+  __shared__ __align__(16) float xs[TT * kMmTokenStride];
+  __shared__ float s_scale[TT];
+  uint32_t rt, tt;
+  q8_mm_tile(blockIdx.x, n_rt, rt, tt);
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int q = lane & 31;
+  const uint32_t row0 = rt * kMmRows + (uint32_t)(wave * 2 + (lane >> 5)) * RT;
+  const uint32_t tok0 = tt * TT;
+  const uint32_t nb = a.n_cols / 32;
+  const uint32_t n_chunks = (a.n_cols + kMmChunkCols - 1) / kMmChunkCols;
+
+  if (FUSE && a.norm_gain != nullptr) {  // per-token rmsnorm scales, one wave per 2 tokens
+#pragma unroll
+    for (int i = 0; i < TT / 4; i++) {
+      const int t = wave * (TT / 4) + i;
+      const uint32_t tok = min(tok0 + t, a.n_tokens - 1);
+      const float s = q8_norm_scale(a, a.x + (size_t)tok * a.n_cols);
+      if (lane == 0) s_scale[t] = s;
+    }
+  }
+
+  const uint8_t* wrow[RT];
+  const uint16_t* srow[RT];
+#pragma unroll
+  for (int r = 0; r < RT; r++) {
+    const uint32_t row = min(row0 + r, a.n_rows - 1);  // past the end: re-read the last row
+    wrow[r] = a.qs + (size_t)row * a.n_cols;
+    srow[r] = a.scales + (size_t)row * nb;
+  }
+
+  float acc[RT][TT];
+#pragma unroll
+  for (int r = 0; r < RT; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) acc[r][t] = 0.f;
+
+  // Leaf q's blocks sit in the even chunks, leaf q + 32's in the odd ones.
+  for (uint32_t c = 0; c < n_chunks; c += 2)
+    q8_mm_chunk<FUSE, RT, TT>(a, c, q, tok0, wrow, srow, xs, s_scale, acc);
+  if (TWO) {
+    float accb[RT][TT];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+      for (int t = 0; t < TT; t++) accb[r][t] = 0.f;
+    for (uint32_t c = 1; c < n_chunks; c += 2)
+      q8_mm_chunk<FUSE, RT, TT>(a, c, q, tok0, wrow, srow, xs, s_scale, accb);
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+      for (int t = 0; t < TT; t++) acc[r][t] = acc[r][t] + accb[r][t];
+  }
+
+  // Outputs o = t * RT + r. The tree's stride 32 (leaf q + leaf q + 32), then
+  // strides 16 .. 1 by recursive halving: at stride s the lane whose bit s is
+  // clear keeps the lower half of its list, its partner the upper half, and
+  // each adds what the other sends. Lane q ends with output q.
+  constexpr int NO = RT * TT;
+  static_assert(NO == 32, "one output per lane after halving");
+  float v[NO];
+#pragma unroll
+  for (int r = 0; r < RT; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+      v[t * RT + r] = acc[r][t];
+  q8_halve<16, NO>(v, q);
+  const uint32_t tok = tok0 + q / RT, row = row0 + q % RT;
+  float out = v[0];
+  if (a.act != nullptr) {  // (gate, up) row pairs: lanes q, q ^ 1 (row0 is a multiple of 4)
+    const float up = shfl_xor(out, 1);
+    if ((q & 1) == 0 && tok < a.n_tokens && row + 1 < a.n_rows)
+      a.act[(size_t)tok * (a.n_rows / 2) + row / 2] = q8_swiglu(out, up);
+    return;
+  }
+  if (tok < a.n_tokens && row < a.n_rows) {
+    const size_t oi = (size_t)tok * a.n_rows + row;
+    if (a.res != nullptr) out = a.res[oi] + out;
+    a.o[oi] = out;
+  }
+}
+
 // Workgroups: one resident wave of them (every CU filled to its occupancy
 // limit, so no workgroup waits for another to finish), never more than there
 // are row groups.
@@ -396,7 +637,21 @@ hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const flo
   }
   const uint32_t nb = n_cols / 32;
   uint32_t gx;
-  if (nb > (uint32_t)kQ8Lanes * kQ8MaxRegBlocks) {
+  const uint32_t n_rt = (n_rows + kMmRows - 1) / kMmRows;
+  const uint32_t n_tt = (n_tokens + kMmTokens - 1) / kMmTokens;
+  if (n_tokens >= FLK_Q8_MM_MIN_TOKENS && best_val == nullptr &&
+      (uint64_t)n_rt * n_tt <= 0x7fffffffu) {
+    gx = n_rt * n_tt;
+    const bool fuse = a.norm_gain != nullptr || a.up != nullptr, two = n_cols > kMmChunkCols;
+    if (fuse && two)
+      hipLaunchKernelGGL((q8_mm_kernel<true, true>), dim3(gx), dim3(kQ8Threads), 0, st, a, n_rt);
+    else if (fuse)
+      hipLaunchKernelGGL((q8_mm_kernel<true, false>), dim3(gx), dim3(kQ8Threads), 0, st, a, n_rt);
+    else if (two)
+      hipLaunchKernelGGL((q8_mm_kernel<false, true>), dim3(gx), dim3(kQ8Threads), 0, st, a, n_rt);
+    else
+      hipLaunchKernelGGL((q8_mm_kernel<false, false>), dim3(gx), dim3(kQ8Threads), 0, st, a, n_rt);
+  } else if (nb > (uint32_t)kQ8Lanes * kQ8MaxRegBlocks) {
     gx = (n_rows + 3) / 4 < 2048u ? (n_rows + 3) / 4 : 2048u;
     hipLaunchKernelGGL(q8_matvec_wide_kernel, dim3(gx, n_tokens), dim3(kQ8Threads), 0, st, a);
   } else if (nb > 192) {

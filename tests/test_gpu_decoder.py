@@ -30,7 +30,9 @@ def dev(a):
 
 
 @pytest.mark.parametrize("rows,cols,n", [(4096, 1024, 1), (1024, 3072, 1), (2048, 1024, 3),
-                                         (300, 8224, 2)])
+                                         (300, 8224, 2),
+                                         # token tiles (8 or more tokens)
+                                         (2048, 1024, 11), (1024, 3072, 9), (300, 8224, 8)])
 def test_matvec_fusions_match_separate_ops(rng, rows, cols, n):
     packed = random_packed(rng, rows, cols)
     w = ops.Q8Matrix.from_packed(packed, rows, cols)
@@ -112,9 +114,9 @@ def test_decode_steps_match_layer_forward_ref(rng):
     layer.free()
 
 
-@pytest.mark.parametrize("n,pos0", [(5, 0), (8, 3)])
+@pytest.mark.parametrize("n,pos0", [(5, 0), (8, 3), (21, 6)])
 def test_prefill_matches_layer_prefill_ref(rng, n, pos0):
-    cfg = DecoderConfig(maxKeys=32, maxPrefill=8)
+    cfg = DecoderConfig(maxKeys=32, maxPrefill=max(8, n))
     w = make_weights(rng, cfg)
     layer = DecoderLayer.create(cfg, w)
     row = cfg.nKvHeads * cfg.headDim
@@ -154,7 +156,8 @@ def test_guards(rng):
     layer.free()
 
 
-@pytest.mark.parametrize("ffn,hid,n", [(3072, 1024, 1), (3072, 1024, 3), (500, 256, 2), (64, 64, 1)])
+@pytest.mark.parametrize("ffn,hid,n", [(3072, 1024, 1), (3072, 1024, 3), (500, 256, 2), (64, 64, 1),
+                                       (3072, 1024, 12), (500, 256, 9)])
 def test_gate_up_swiglu_matches_separate_ops(rng, ffn, hid, n):
     gate = random_packed(rng, ffn, hid)
     up = random_packed(rng, ffn, hid)

@@ -6,7 +6,9 @@ output must equal the oracle's (fused=True) exactly. Shapes cover the Qwen3
 projections (q 2048x1024, k/v 1024x1024, o 1024x2048, gate/up 3072x1024,
 down 1024x3072, LM head 151936x1024), every lanes-per-row layout (1..64 and
 2-4 blocks per lane), the wide fallback (> 8192 columns), batched tokens and
-the f16 scale edge cases (subnormal, exponent 31).
+the f16 scale edge cases (subnormal, exponent 31). Batches of 8 or more
+tokens go through the tile kernel that reuses each weight block across
+tokens; it is held to the same exactness.
 """
 from __future__ import annotations
 
@@ -60,6 +62,21 @@ def test_batched_tokens(rng, n_tokens):
     got = run_gpu(packed, x, rows, cols, n_tokens)
     want = oracle.q8_matvec(packed, x, rows, cols, 64, fused=True)
     assert np.array_equal(got, want)
+
+
+@pytest.mark.parametrize("rows,cols,n_tokens", [
+    (96, 1024, 8), (100, 1024, 13),                 # one chunk; ragged row and token tiles
+    (1024, 2048, 9), (33, 1536, 8),                 # two leaves per lane (the second partial)
+    (70, 3072, 17), (13, 8224, 8), (24, 8192, 10),  # three and more chunks
+    (40, 512, 10), (5, 32, 8), (3, 96, 11),         # fewer blocks than lanes
+])
+def test_token_tiles_match_oracle(rng, rows, cols, n_tokens):
+    """Batches of 8 or more tokens take the weight-reusing tile kernel; its
+    sums keep the coop(64) order, so it is exact too."""
+    packed, x = problem(rng, rows, cols, n_tokens)
+    got = run_gpu(packed, x, rows, cols, n_tokens)
+    want = oracle.q8_matvec(packed, x, rows, cols, 64, fused=True)
+    assert np.array_equal(got, want), np.flatnonzero(got != want)[:8]
 
 
 def random_packed(rng, rows, cols):
