@@ -19,8 +19,10 @@
 // exact zeros), so a wave covers 64 / P rows at once (2 for 1024 columns).
 // Lane l's x slice (blocks l, l + 64, ...) is the same for every row: it is
 // loaded into registers once per wave and the row loop streams only the
-// weights, several row groups in flight. Tokens of a batch ride on grid y
-// (q8_coop.wgsl:28-35); each re-reads the weights, from L2 when they fit.
+// weights, several row groups in flight. Tokens of a small batch ride on grid
+// y (q8_coop.wgsl:28-35) and each re-reads the weights; batches of 8 or more
+// tokens take the tile kernels further down, which reuse every weight block
+// for 8 tokens.
 #include "common.hpp"
 
 namespace flk {
@@ -38,8 +40,13 @@ constexpr int kQ8Threads = 256;   // 4 waves
 #ifndef FLK_Q8_MM_MIN_TOKENS
 #define FLK_Q8_MM_MIN_TOKENS 8
 #endif
+// Waves per SIMD the tile kernel's registers are limited to (rows of more
+// than 1024 columns keep a second set of partials).
 #ifndef FLK_Q8_MM_WAVES
-#define FLK_Q8_MM_WAVES 2  // waves per SIMD the tile kernel is register-limited to
+#define FLK_Q8_MM_WAVES 2
+#endif
+#ifndef FLK_Q8_MM_WAVES1
+#define FLK_Q8_MM_WAVES1 3  // rows of at most 1024 columns
 #endif
 template <int NB>
 constexpr int q8_unroll() { return NB == 1 ? FLK_Q8_UNROLL : (NB == 2 ? 2 : 1); }
@@ -103,27 +110,27 @@ __device__ __forceinline__ void q8_fused_block(const Q8Args& a, const float* xt,
   }
 }
 
-// rmsnorm scale of a token's x (rmsnorm.wgsl:45-66), per wave and without a
-// barrier: lane l holds the reference's partials l and l + 64 (stride-128
-// fma32 sums), their sum is the tree's stride-64 step, and the xor butterfly
-// over the wave is its strides 32 .. 1; scale = 1 / sqrt(mean + eps) rounded
-// once. (A workgroup barrier would also wait for the weight loads already in
-// flight.) Returns 1 when there is no norm.
-__device__ __forceinline__ float q8_norm_scale(const Q8Args& a, const float* xt) {
-  if (a.norm_gain == nullptr) return 1.f;
+// rmsnorm scale of a token's n elements, read through ld(i) from any memory
+// (rmsnorm.wgsl:45-66), per wave and without a barrier: lane l holds the
+// reference's partials l and l + 64 (stride-128 fma32 sums), their sum is the
+// tree's stride-64 step, and the xor butterfly over the wave is its strides
+// 32 .. 1; scale = 1 / sqrt(mean + eps) rounded once. (A workgroup barrier
+// would also wait for the weight loads already in flight.)
+template <class LOAD>
+__device__ __forceinline__ float q8_rms_scale(uint32_t n, float eps, LOAD ld) {
   const uint32_t l = threadIdx.x & 63;
   // Elements l + 64k: even k feed partial l, odd k partial l + 64. Eight are
   // loaded before any is used (a load-use loop would serialise the
   // latencies); past the end they read 0, which adds exactly nothing.
   constexpr int kB = 8;
   float p0 = 0.f, p1 = 0.f;
-  for (uint32_t base = l; base < a.n_cols; base += 64 * kB) {
+  for (uint32_t base = l; base < n; base += 64 * kB) {
     float v[kB];
 #pragma unroll
     for (int k = 0; k < kB; k++) {
       const uint32_t i = base + 64 * k;
-      v[k] = xt[min(i, a.n_cols - 1)];
-      v[k] = i < a.n_cols ? v[k] : 0.f;
+      v[k] = ld(min(i, n - 1));
+      v[k] = i < n ? v[k] : 0.f;
     }
 #pragma unroll
     for (int k = 0; k < kB; k += 2) {
@@ -134,8 +141,14 @@ __device__ __forceinline__ float q8_norm_scale(const Q8Args& a, const float* xt)
   float sum = p0 + p1;
 #pragma unroll
   for (int m = 32; m >= 1; m >>= 1) sum += shfl_xor(sum, m);
-  const float mean = sum / (float)a.n_cols;
-  return rsqrt_once(mean + a.norm_eps);
+  const float mean = sum / (float)n;
+  return rsqrt_once(mean + eps);
+}
+
+// The scale of token row xt in global memory; 1 when there is no norm.
+__device__ __forceinline__ float q8_norm_scale(const Q8Args& a, const float* xt) {
+  if (a.norm_gain == nullptr) return 1.f;
+  return q8_rms_scale(a.n_cols, a.norm_eps, [xt](uint32_t i) { return xt[i]; });
 }
 
 // halfToF32 (kernels/lib.ts:28-33): exact for every finite f16 (subnormals
@@ -349,57 +362,91 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
 // x is staged through LDS in chunks of 32 blocks (1024 columns) with any input
 // fusion applied there; each lane reads its block of every token (blocks
 // padded to 36 floats so the 16 lanes of a read phase hit distinct banks).
-// Weights come straight from memory, requested before the staging barrier.
-constexpr int kMmRowsPerSlot = 4;
-constexpr int kMmTokens = 8;
+// Weights come straight from memory. Rows of one chunk (q/k/v, gate/up at
+// hidden 1024) stage their token tile once per workgroup -- rmsnorm scales
+// included, computed from the staged rows -- and stream kMmRowTiles row tiles
+// through it with no barrier in between; longer rows take one tile per
+// workgroup and restage per chunk.
+#ifndef FLK_Q8_MM_RT
+#define FLK_Q8_MM_RT 4
+#endif
+constexpr int kMmRowsPerSlot = FLK_Q8_MM_RT;
+constexpr int kMmTokens = 32 / FLK_Q8_MM_RT;  // 32 outputs per lane
 constexpr int kMmRows = (kQ8Threads / kWave) * 2 * kMmRowsPerSlot;  // 32
 constexpr int kMmPad = 36;
 constexpr int kMmChunkCols = 1024;
 constexpr int kMmTokenStride = 32 * kMmPad;  // floats per staged token
+#ifndef FLK_Q8_MM_ROW_TILES
+#define FLK_Q8_MM_ROW_TILES 8
+#endif
+// Row tiles one workgroup streams through its staged tokens (rows of one chunk).
+constexpr uint32_t kMmRowTiles = FLK_Q8_MM_ROW_TILES;
 
 // One block of RT rows (weights w0/w1, scales sc) against the staged tokens,
-// folded into acc[r][t] (q8_coop.wgsl:105-112 per output).
+// folded into acc[r][t] (q8_coop.wgsl:105-112 per output). Per word pair g,
+// the quants of every row are converted once and used for every token (more
+// tokens than rows), or the x of every token is loaded once and used for
+// every row (more rows than tokens).
 template <int RT, int TT>
 __device__ __forceinline__ void q8_mm_block(float (&acc)[RT][TT], const uint4 (&w0)[RT],
                                             const uint4 (&w1)[RT], const float (&sc)[RT],
                                             const float* xb) {
 #pragma unroll
   for (int g = 0; g < 4; g++) {
-    float qf[RT][8];
-#pragma unroll
-    for (int r = 0; r < RT; r++) {
+    auto quants = [&](int r, float (&qf)[8]) {
       const uint32_t wa = g == 0 ? w0[r].x : g == 1 ? w0[r].z : g == 2 ? w1[r].x : w1[r].z;
       const uint32_t wb = g == 0 ? w0[r].y : g == 1 ? w0[r].w : g == 2 ? w1[r].y : w1[r].w;
 #pragma unroll
       for (int k = 0; k < 4; k++) {
-        qf[r][k] = q8_quant(wa, k);
-        qf[r][4 + k] = q8_quant(wb, k);
+        qf[k] = q8_quant(wa, k);
+        qf[4 + k] = q8_quant(wb, k);
       }
-    }
+    };
+    auto fold = [&](int r, int t, const float (&qf)[8], float4 xa, float4 xc) {
+      float d0 = qf[0] * xa.x;
+      d0 = __builtin_fmaf(qf[1], xa.y, d0);
+      d0 = __builtin_fmaf(qf[2], xa.z, d0);
+      d0 = __builtin_fmaf(qf[3], xa.w, d0);
+      float d1 = qf[4] * xc.x;
+      d1 = __builtin_fmaf(qf[5], xc.y, d1);
+      d1 = __builtin_fmaf(qf[6], xc.z, d1);
+      d1 = __builtin_fmaf(qf[7], xc.w, d1);
+      acc[r][t] = __builtin_fmaf(sc[r], d0 + d1, acc[r][t]);
+    };
+    if constexpr (TT >= RT) {
+      float qf[RT][8];
 #pragma unroll
-    for (int t = 0; t < TT; t++) {
-      const float4 xa = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g);
-      const float4 xc = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g + 4);
+      for (int r = 0; r < RT; r++) quants(r, qf[r]);
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        const float4 xa = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g);
+        const float4 xc = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g + 4);
+#pragma unroll
+        for (int r = 0; r < RT; r++) fold(r, t, qf[r], xa, xc);
+      }
+    } else {
+      float4 xa[TT], xc[TT];
+#pragma unroll
+      for (int t = 0; t < TT; t++) {
+        xa[t] = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g);
+        xc[t] = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g + 4);
+      }
 #pragma unroll
       for (int r = 0; r < RT; r++) {
-        float d0 = qf[r][0] * xa.x;
-        d0 = __builtin_fmaf(qf[r][1], xa.y, d0);
-        d0 = __builtin_fmaf(qf[r][2], xa.z, d0);
-        d0 = __builtin_fmaf(qf[r][3], xa.w, d0);
-        float d1 = qf[r][4] * xc.x;
-        d1 = __builtin_fmaf(qf[r][5], xc.y, d1);
-        d1 = __builtin_fmaf(qf[r][6], xc.z, d1);
-        d1 = __builtin_fmaf(qf[r][7], xc.w, d1);
-        acc[r][t] = __builtin_fmaf(sc[r], d0 + d1, acc[r][t]);
+        float qf[8];
+        quants(r, qf);
+#pragma unroll
+        for (int t = 0; t < TT; t++) fold(r, t, qf, xa[t], xc[t]);
       }
     }
   }
 }
 
-// Tile (row tile, token tile) of workgroup `id`. When the row tiles split
-// evenly over the 8 XCDs (workgroups go to XCDs round-robin by id), XCD x
-// takes a contiguous eighth of the rows and walks it token tile by token
-// tile, so its share of the weights stays in its own L2 while x streams.
+// Tile (row tile or row-tile group, token tile) of workgroup `id`. When the
+// row tiles split evenly over the 8 XCDs (workgroups go to XCDs round-robin
+// by id), XCD x takes a contiguous eighth of the rows and walks it token tile
+// by token tile, so its share of the weights stays in its own L2 while x
+// streams.
 __device__ __forceinline__ void q8_mm_tile(uint32_t id, uint32_t n_rt, uint32_t& rt,
                                            uint32_t& tt) {
   if (n_rt % 8 == 0) {
@@ -412,52 +459,89 @@ __device__ __forceinline__ void q8_mm_tile(uint32_t id, uint32_t n_rt, uint32_t&
   }
 }
 
-// Chunk c (blocks 32c .. 32c + 31) of a tile: lane q's weights for block
-// 32c + q are requested, x's columns 1024c .. 1024c + 1023 of the tile's tokens
-// are staged (with the input fusion), and the block is folded into acc.
-template <bool FUSE, int RT, int TT>
-__device__ __forceinline__ void q8_mm_chunk(const Q8Args& a, uint32_t c, int q, uint32_t tok0,
-                                            const uint8_t* const (&wrow)[RT],
-                                            const uint16_t* const (&srow)[RT], float* xs,
-                                            const float* s_scale, float (&acc)[RT][TT]) {
-  const uint32_t nb = a.n_cols / 32;
-  const uint32_t b = 32 * c + q;
-  const uint32_t bl = min(b, nb - 1);
+// Input fusions of the tile kernel.
+enum Q8MmFuse { kMmPlain = 0, kMmNorm = 1, kMmSwiglu = 2 };
+
+// Lane q's weights of chunk c (block 32c + q; past the row's end the last
+// block is re-read and not used) for RT rows.
+template <int RT>
+struct Q8MmWeights {
   uint4 w0[RT], w1[RT];
   float sc[RT];
+};
+template <int RT>
+__device__ __forceinline__ Q8MmWeights<RT> q8_mm_weights(const Q8Args& a, uint32_t c, int q,
+                                                         const uint8_t* const (&wrow)[RT],
+                                                         const uint16_t* const (&srow)[RT]) {
+  const uint32_t nb = a.n_cols / 32;
+  const uint32_t bl = min(32 * c + q, nb - 1);
+  Q8MmWeights<RT> w;
 #pragma unroll
   for (int r = 0; r < RT; r++) {
     const uint4* src = reinterpret_cast<const uint4*>(wrow[r] + 32 * (size_t)bl);
-    w0[r] = src[0];
-    w1[r] = src[1];
-    sc[r] = q8_scale(srow[r][bl]);
+    w.w0[r] = src[0];
+    w.w1[r] = src[1];
+    w.sc[r] = q8_scale(srow[r][bl]);
   }
-  __syncthreads();  // the previous chunk's reads are done (and s_scale is visible)
-  // TT tokens x 256 float4s, 8 per thread.
+  return w;
+}
+
+// Stages x's columns 1024c .. 1024c + 1023 of tokens tok0 .. tok0 + TT - 1
+// into xs (with the input fusion) and ends with a barrier; the caller has
+// made sure no wave still reads xs. NORM_HERE (rows of one chunk): the
+// rmsnorm scales are computed here from the staged raw rows; otherwise
+// s_scale already holds them.
+template <int FUSE, bool NORM_HERE, int TT>
+__device__ __forceinline__ void q8_mm_stage(const Q8Args& a, uint32_t c, uint32_t tok0, float* xs,
+                                            float* s_scale) {
+  // Thread j stages float4 j (columns 1024c + 4j ..) of every token; every
+  // load is issued before any is used. Columns past the row's end are
+  // clamped on load and not stored.
+  static_assert(kQ8Threads == kMmChunkCols / 4, "one float4 column per thread");
+  const uint32_t j = threadIdx.x;
+  const uint32_t col = min(kMmChunkCols * c + 4 * j, a.n_cols - 4);
+  float* dst = xs + (j / 8) * kMmPad + 4 * (j % 8);
+  float4 v[TT], y[TT];
 #pragma unroll
-  for (int k = 0; k < TT * (kMmChunkCols / 4) / kQ8Threads; k++) {
-    const uint32_t f = threadIdx.x + kQ8Threads * k;
-    const uint32_t t = f / (kMmChunkCols / 4), j = f % (kMmChunkCols / 4);
-    const uint32_t col = kMmChunkCols * c + 4 * j;
-    if (col >= a.n_cols) continue;
-    const uint32_t tok = min(tok0 + t, a.n_tokens - 1);
-    const size_t off = (size_t)tok * a.n_cols + col;
-    float4 v = *reinterpret_cast<const float4*>(a.x + off);
-    if (FUSE) {
-      if (a.norm_gain != nullptr) {
-        const float s = s_scale[t];
-        const float4 gn = *reinterpret_cast<const float4*>(a.norm_gain + col);
-        v = make_float4((v.x * s) * gn.x, (v.y * s) * gn.y, (v.z * s) * gn.z, (v.w * s) * gn.w);
-      } else {
-        const float4 u = *reinterpret_cast<const float4*>(a.up + off);
-        v = make_float4(q8_swiglu(v.x, u.x), q8_swiglu(v.y, u.y), q8_swiglu(v.z, u.z),
-                        q8_swiglu(v.w, u.w));
-      }
+  for (int t = 0; t < TT; t++) {
+    const size_t off = (size_t)min(tok0 + t, a.n_tokens - 1) * a.n_cols + col;
+    v[t] = *reinterpret_cast<const float4*>(a.x + off);
+    if (FUSE == kMmSwiglu) y[t] = *reinterpret_cast<const float4*>(a.up + off);
+  }
+  float4 gn = make_float4(0.f, 0.f, 0.f, 0.f);
+  if (FUSE == kMmNorm) gn = *reinterpret_cast<const float4*>(a.norm_gain + col);
+  const bool store = kMmChunkCols * c + 4 * j < a.n_cols;
+  if (NORM_HERE) {
+    // Raw rows first; each wave then takes the scales of TT / 4 tokens.
+#pragma unroll
+    for (int t = 0; t < TT; t++)
+      if (store) *reinterpret_cast<float4*>(dst + t * kMmTokenStride) = v[t];
+    __syncthreads();
+    const int wave = threadIdx.x >> 6;
+#pragma unroll
+    for (int i = 0; i < TT / 4; i++) {
+      const int t = wave * (TT / 4) + i;
+      const float* row = xs + t * kMmTokenStride;
+      const float s = q8_rms_scale(a.n_cols, a.norm_eps,
+                                   [row](uint32_t e) { return row[(e >> 5) * kMmPad + (e & 31)]; });
+      if ((threadIdx.x & 63) == 0) s_scale[t] = s;
     }
-    *reinterpret_cast<float4*>(xs + t * kMmTokenStride + (j / 8) * kMmPad + 4 * (j % 8)) = v;
+    __syncthreads();
+  }
+#pragma unroll
+  for (int t = 0; t < TT; t++) {
+    float4 u = v[t];
+    if (FUSE == kMmNorm) {
+      const float s = s_scale[t];
+      u = make_float4((u.x * s) * gn.x, (u.y * s) * gn.y, (u.z * s) * gn.z, (u.w * s) * gn.w);
+    } else if (FUSE == kMmSwiglu) {
+      const float4 gy = y[t];
+      u = make_float4(q8_swiglu(u.x, gy.x), q8_swiglu(u.y, gy.y), q8_swiglu(u.z, gy.z),
+                      q8_swiglu(u.w, gy.w));
+    }
+    if (store) *reinterpret_cast<float4*>(dst + t * kMmTokenStride) = u;
   }
   __syncthreads();
-  if (b < nb) q8_mm_block<RT, TT>(acc, w0, w1, sc, xs + q * kMmPad);
 }
 
 // One recursive-halving step over v[0 .. N): lanes with bit S clear keep
@@ -482,8 +566,91 @@ __device__ __forceinline__ void q8_halve(float (&v)[32], int q) {
 }
 
 // TWO: the rows have more than 32 blocks (leaf q + 32 exists).
-template <bool FUSE, bool TWO>
-__global__ __launch_bounds__(kQ8Threads, TWO ? FLK_Q8_MM_WAVES : FLK_Q8_MM_WAVES + 1) void q8_mm_kernel(Q8Args a, uint32_t n_rt) {
+// Outputs o = t * RT + r of acc: the tree's strides 16 .. 1 by recursive
+// halving (at stride s the lane whose bit s is clear keeps the lower half of
+// its list, its partner the upper half, and each adds what the other sends;
+// lane q ends with output q), then the epilogue: SwiGLU of (gate, up) row
+// pairs into act, or res + sum into o.
+template <int RT, int TT>
+__device__ __forceinline__ void q8_mm_finish(const Q8Args& a, const float (&acc)[RT][TT], int q,
+                                             uint32_t row0, uint32_t tok0) {
+  constexpr int NO = RT * TT;
+  static_assert(NO == 32, "one output per lane after halving");
+  float v[NO];
+#pragma unroll
+  for (int r = 0; r < RT; r++)
+#pragma unroll
+    for (int t = 0; t < TT; t++) v[t * RT + r] = acc[r][t];
+  q8_halve<16, NO>(v, q);
+  const uint32_t tok = tok0 + q / RT, row = row0 + q % RT;
+  float out = v[0];
+  if (a.act != nullptr) {  // (gate, up) row pairs: lanes q, q ^ 1 (row0 is a multiple of 4)
+    const float up = shfl_xor(out, 1);
+    if ((q & 1) == 0 && tok < a.n_tokens && row + 1 < a.n_rows)
+      a.act[(size_t)tok * (a.n_rows / 2) + row / 2] = q8_swiglu(out, up);
+  } else if (tok < a.n_tokens && row < a.n_rows) {
+    const size_t oi = (size_t)tok * a.n_rows + row;
+    if (a.res != nullptr) out = a.res[oi] + out;
+    a.o[oi] = out;
+  }
+}
+
+// Row pointers of lane slot (wave, lane >> 5) in row tile rt (rows past the
+// end re-read the last row and are not stored).
+template <int RT>
+__device__ __forceinline__ uint32_t q8_mm_rows(const Q8Args& a, uint32_t rt,
+                                               const uint8_t* (&wrow)[RT],
+                                               const uint16_t* (&srow)[RT]) {
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const uint32_t row0 = rt * kMmRows + (uint32_t)(wave * 2 + (lane >> 5)) * RT;
+  const uint32_t nb = a.n_cols / 32;
+#pragma unroll
+  for (int r = 0; r < RT; r++) {
+    const uint32_t row = min(row0 + r, a.n_rows - 1);
+    wrow[r] = a.qs + (size_t)row * a.n_cols;
+    srow[r] = a.scales + (size_t)row * nb;
+  }
+  return row0;
+}
+
+// Rows of one chunk (at most 1024 columns): a workgroup stages its token
+// tile once and streams kMmRowTiles row tiles through it, with no barrier
+// between them.
+template <int FUSE>
+__global__ __launch_bounds__(kQ8Threads, FLK_Q8_MM_WAVES1) void q8_mm1_kernel(Q8Args a,
+                                                                              uint32_t n_rg) {
+  constexpr int RT = kMmRowsPerSlot, TT = kMmTokens;
+  __shared__ __align__(16) float xs[TT * kMmTokenStride];
+  __shared__ float s_scale[TT];
+  uint32_t rg, tt;
+  q8_mm_tile(blockIdx.x, n_rg, rg, tt);
+  const int q = threadIdx.x & 31;
+  const uint32_t tok0 = tt * TT;
+  const uint32_t n_rt = (a.n_rows + kMmRows - 1) / kMmRows;
+  const uint32_t rt_end = min(n_rt, (rg + 1) * kMmRowTiles);
+  q8_mm_stage<FUSE, FUSE == kMmNorm, TT>(a, 0, tok0, xs, s_scale);
+  const bool live = (uint32_t)q < a.n_cols / 32;
+  for (uint32_t rt = rg * kMmRowTiles; rt < rt_end; rt++) {
+    const uint8_t* wrow[RT];
+    const uint16_t* srow[RT];
+    const uint32_t row0 = q8_mm_rows<RT>(a, rt, wrow, srow);
+    const Q8MmWeights<RT> w = q8_mm_weights<RT>(a, 0, q, wrow, srow);
+    float acc[RT][TT];
+#pragma unroll
+    for (int r = 0; r < RT; r++)
+#pragma unroll
+      for (int t = 0; t < TT; t++) acc[r][t] = 0.f;
+    if (live) q8_mm_block<RT, TT>(acc, w.w0, w.w1, w.sc, xs + q * kMmPad);
+    q8_mm_finish<RT, TT>(a, acc, q, row0, tok0);
+  }
+}
+
+// Rows of more than one chunk: a workgroup owns one tile; leaf q's blocks
+// sit in the even chunks, leaf q + 32's in the odd ones (a second set of
+// partials, added at the end: the tree's stride 32).
+template <int FUSE>
+__global__ __launch_bounds__(kQ8Threads, FLK_Q8_MM_WAVES) void q8_mm_kernel(Q8Args a,
+                                                                            uint32_t n_rt) {
   constexpr int RT = kMmRowsPerSlot, TT = kMmTokens;
   __shared__ __align__(16) float xs[TT * kMmTokenStride];
   __shared__ float s_scale[TT];
@@ -491,12 +658,10 @@ __global__ __launch_bounds__(kQ8Threads, TWO ? FLK_Q8_MM_WAVES : FLK_Q8_MM_WAVES
   q8_mm_tile(blockIdx.x, n_rt, rt, tt);
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int q = lane & 31;
-  const uint32_t row0 = rt * kMmRows + (uint32_t)(wave * 2 + (lane >> 5)) * RT;
   const uint32_t tok0 = tt * TT;
   const uint32_t nb = a.n_cols / 32;
   const uint32_t n_chunks = (a.n_cols + kMmChunkCols - 1) / kMmChunkCols;
-
-  if (FUSE && a.norm_gain != nullptr) {  // per-token rmsnorm scales, one wave per 2 tokens
+  if (FUSE == kMmNorm) {  // per-token rmsnorm scales, TT / 4 tokens per wave
 #pragma unroll
     for (int i = 0; i < TT / 4; i++) {
       const int t = wave * (TT / 4) + i;
@@ -505,65 +670,32 @@ __global__ __launch_bounds__(kQ8Threads, TWO ? FLK_Q8_MM_WAVES : FLK_Q8_MM_WAVES
       if (lane == 0) s_scale[t] = s;
     }
   }
-
   const uint8_t* wrow[RT];
   const uint16_t* srow[RT];
-#pragma unroll
-  for (int r = 0; r < RT; r++) {
-    const uint32_t row = min(row0 + r, a.n_rows - 1);  // past the end: re-read the last row
-    wrow[r] = a.qs + (size_t)row * a.n_cols;
-    srow[r] = a.scales + (size_t)row * nb;
-  }
+  const uint32_t row0 = q8_mm_rows<RT>(a, rt, wrow, srow);
 
-  float acc[RT][TT];
+  float acc[RT][TT], accb[RT][TT];
 #pragma unroll
   for (int r = 0; r < RT; r++)
 #pragma unroll
-    for (int t = 0; t < TT; t++) acc[r][t] = 0.f;
-
-  // Leaf q's blocks sit in the even chunks, leaf q + 32's in the odd ones.
-  for (uint32_t c = 0; c < n_chunks; c += 2)
-    q8_mm_chunk<FUSE, RT, TT>(a, c, q, tok0, wrow, srow, xs, s_scale, acc);
-  if (TWO) {
-    float accb[RT][TT];
-#pragma unroll
-    for (int r = 0; r < RT; r++)
-#pragma unroll
-      for (int t = 0; t < TT; t++) accb[r][t] = 0.f;
-    for (uint32_t c = 1; c < n_chunks; c += 2)
-      q8_mm_chunk<FUSE, RT, TT>(a, c, q, tok0, wrow, srow, xs, s_scale, accb);
-#pragma unroll
-    for (int r = 0; r < RT; r++)
-#pragma unroll
-      for (int t = 0; t < TT; t++) acc[r][t] = acc[r][t] + accb[r][t];
+    for (int t = 0; t < TT; t++) acc[r][t] = accb[r][t] = 0.f;
+  for (uint32_t c = 0; c < n_chunks; c += 2) {
+    const Q8MmWeights<RT> w = q8_mm_weights<RT>(a, c, q, wrow, srow);
+    __syncthreads();  // the previous chunk's reads are done (and s_scale is visible)
+    q8_mm_stage<FUSE, false, TT>(a, c, tok0, xs, s_scale);
+    if (32 * c + q < nb) q8_mm_block<RT, TT>(acc, w.w0, w.w1, w.sc, xs + q * kMmPad);
   }
-
-  // Outputs o = t * RT + r. The tree's stride 32 (leaf q + leaf q + 32), then
-  // strides 16 .. 1 by recursive halving: at stride s the lane whose bit s is
-  // clear keeps the lower half of its list, its partner the upper half, and
-  // each adds what the other sends. Lane q ends with output q.
-  constexpr int NO = RT * TT;
-  static_assert(NO == 32, "one output per lane after halving");
-  float v[NO];
+  for (uint32_t c = 1; c < n_chunks; c += 2) {
+    const Q8MmWeights<RT> w = q8_mm_weights<RT>(a, c, q, wrow, srow);
+    __syncthreads();
+    q8_mm_stage<FUSE, false, TT>(a, c, tok0, xs, s_scale);
+    if (32 * c + q < nb) q8_mm_block<RT, TT>(accb, w.w0, w.w1, w.sc, xs + q * kMmPad);
+  }
 #pragma unroll
   for (int r = 0; r < RT; r++)
 #pragma unroll
-    for (int t = 0; t < TT; t++)
-      v[t * RT + r] = acc[r][t];
-  q8_halve<16, NO>(v, q);
-  const uint32_t tok = tok0 + q / RT, row = row0 + q % RT;
-  float out = v[0];
-  if (a.act != nullptr) {  // (gate, up) row pairs: lanes q, q ^ 1 (row0 is a multiple of 4)
-    const float up = shfl_xor(out, 1);
-    if ((q & 1) == 0 && tok < a.n_tokens && row + 1 < a.n_rows)
-      a.act[(size_t)tok * (a.n_rows / 2) + row / 2] = q8_swiglu(out, up);
-    return;
-  }
-  if (tok < a.n_tokens && row < a.n_rows) {
-    const size_t oi = (size_t)tok * a.n_rows + row;
-    if (a.res != nullptr) out = a.res[oi] + out;
-    a.o[oi] = out;
-  }
+    for (int t = 0; t < TT; t++) acc[r][t] = acc[r][t] + accb[r][t];
+  q8_mm_finish<RT, TT>(a, acc, q, row0, tok0);
 }
 
 // Workgroups: one resident wave of them (every CU filled to its occupancy
@@ -639,18 +771,21 @@ hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const flo
   uint32_t gx;
   const uint32_t n_rt = (n_rows + kMmRows - 1) / kMmRows;
   const uint32_t n_tt = (n_tokens + kMmTokens - 1) / kMmTokens;
+  const bool one = n_cols <= (uint32_t)kMmChunkCols;
+  const uint32_t n_rg = one ? (n_rt + kMmRowTiles - 1) / kMmRowTiles : n_rt;
   if (n_tokens >= FLK_Q8_MM_MIN_TOKENS && best_val == nullptr &&
-      (uint64_t)n_rt * n_tt <= 0x7fffffffu) {
-    gx = n_rt * n_tt;
-    const bool fuse = a.norm_gain != nullptr || a.up != nullptr, two = n_cols > kMmChunkCols;
-    if (fuse && two)
-      hipLaunchKernelGGL((q8_mm_kernel<true, true>), dim3(gx), dim3(kQ8Threads), 0, st, a, n_rt);
-    else if (fuse)
-      hipLaunchKernelGGL((q8_mm_kernel<true, false>), dim3(gx), dim3(kQ8Threads), 0, st, a, n_rt);
-    else if (two)
-      hipLaunchKernelGGL((q8_mm_kernel<false, true>), dim3(gx), dim3(kQ8Threads), 0, st, a, n_rt);
+      (uint64_t)n_rg * n_tt <= 0x7fffffffu) {
+    gx = n_rg * n_tt;
+    const int fuse = a.norm_gain != nullptr ? kMmNorm : (a.up != nullptr ? kMmSwiglu : kMmPlain);
+    auto go = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, dim3(gx), dim3(kQ8Threads), 0, st, a, n_rg);
+    };
+    if (fuse == kMmNorm)
+      one ? go(q8_mm1_kernel<kMmNorm>) : go(q8_mm_kernel<kMmNorm>);
+    else if (fuse == kMmSwiglu)
+      one ? go(q8_mm1_kernel<kMmSwiglu>) : go(q8_mm_kernel<kMmSwiglu>);
     else
-      hipLaunchKernelGGL((q8_mm_kernel<false, false>), dim3(gx), dim3(kQ8Threads), 0, st, a, n_rt);
+      one ? go(q8_mm1_kernel<kMmPlain>) : go(q8_mm_kernel<kMmPlain>);
   } else if (nb > (uint32_t)kQ8Lanes * kQ8MaxRegBlocks) {
     gx = (n_rows + 3) / 4 < 2048u ? (n_rows + 3) / 4 : 2048u;
     hipLaunchKernelGGL(q8_matvec_wide_kernel, dim3(gx, n_tokens), dim3(kQ8Threads), 0, st, a);
