@@ -467,6 +467,8 @@ int32_t flk_q8_matvec_ex(const int8_t* qs, const uint16_t* scales, const float* 
     return fail(FLK_ERR_ARG, "q8_matvec_ex: eps must be >= 0");
   FLK_ALIGNED(qs);
   FLK_ALIGNED(x);
+  if (norm_gain != nullptr) FLK_ALIGNED(norm_gain);
+  if (up != nullptr) FLK_ALIGNED(up);
   if (reinterpret_cast<uintptr_t>(scales) % 2 != 0)
     return fail(FLK_ERR_ARG, "scales must be 2-byte aligned");
   Q8Fuse f;
@@ -496,6 +498,7 @@ int32_t flk_q8_gate_up_swiglu(const int8_t* qs, const uint16_t* scales, const fl
     return fail(FLK_ERR_ARG, "gate_up_swiglu: eps must be >= 0");
   FLK_ALIGNED(qs);
   FLK_ALIGNED(x);
+  if (norm_gain != nullptr) FLK_ALIGNED(norm_gain);
   if (reinterpret_cast<uintptr_t>(scales) % 2 != 0)
     return fail(FLK_ERR_ARG, "scales must be 2-byte aligned");
   Q8Fuse f;

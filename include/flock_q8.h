@@ -41,10 +41,12 @@ int32_t flk_q8_matvec(const int8_t* qs, const uint16_t* scales, const float* x, 
  *     (elementwise.wgsl swiglu; up is [n_tokens][n_cols]) -- before ffn_down;
  *   res != NULL: o = res + W x (elementwise.wgsl add; res is
  *     [n_tokens][n_rows], may equal o) -- the residual adds.
- * norm_gain and up are exclusive. Results are bit-identical to the separate
- * ops (rmsnormRef / swigluRef / addRef, then cpuMatmulQ8F32 coop(64)) except
- * that swiglu's exp is evaluated in f64 and rounded once, as the CPU
- * reference does (the WGSL kernel uses f32 exp). */
+ * norm_gain and up are exclusive and, like x, 16-byte aligned. Results are
+ * bit-identical to the separate ops (rmsnormRef / swigluRef / addRef, then
+ * cpuMatmulQ8F32 coop(64)) except that swiglu's exp is evaluated in f64 and
+ * rounded once, as the CPU reference does (the WGSL kernel uses f32 exp).
+ * Batches of 8 or more tokens reuse each weight block across tokens; the
+ * results are the same. */
 int32_t flk_q8_matvec_ex(const int8_t* qs, const uint16_t* scales, const float* x, float* o,
                          uint32_t n_rows, uint32_t n_cols, uint32_t n_tokens,
                          const float* norm_gain, float norm_eps, const float* up,

@@ -143,6 +143,16 @@ def test_q8_matvec_guards():
     assert rc == _lib.FLK_ERR_ARG and "aligned" in msg
     rc, msg = code_and_msg(L.flk_q8_matvec(None, FAKE, FAKE, FAKE, 16, 64, 1))
     assert rc == _lib.FLK_ERR_ARG and "null" in msg
+    # The fused inputs are read as float4s too.
+    rc, msg = code_and_msg(L.flk_q8_matvec_ex(FAKE, FAKE, FAKE, FAKE, 16, 64, 8, FAKE + 4, 1e-6,
+                                              None, None))
+    assert rc == _lib.FLK_ERR_ARG and "norm_gain" in msg and "aligned" in msg
+    rc, msg = code_and_msg(L.flk_q8_matvec_ex(FAKE, FAKE, FAKE, FAKE, 16, 64, 8, None, 0.0,
+                                              FAKE + 8, None))
+    assert rc == _lib.FLK_ERR_ARG and "up" in msg and "aligned" in msg
+    rc, msg = code_and_msg(L.flk_q8_gate_up_swiglu(FAKE, FAKE, FAKE, FAKE, 16, 64, 8, FAKE + 12,
+                                                   1e-6))
+    assert rc == _lib.FLK_ERR_ARG and "norm_gain" in msg and "aligned" in msg
 
 
 def test_q8_split_matches_oracle():
