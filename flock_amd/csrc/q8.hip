@@ -364,8 +364,8 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
 // padded to 36 floats so the 16 lanes of a read phase hit distinct banks).
 // Weights come straight from memory. Rows of one chunk (q/k/v, gate/up at
 // hidden 1024) stage their token tile once per workgroup -- rmsnorm scales
-// included, computed from the staged rows -- and stream kMmRowTiles row tiles
-// through it with no barrier in between; longer rows take one tile per
+// included, computed from the staged rows -- and stream up to kMmRowTiles row
+// tiles// through it with no barrier in between; longer rows take one tile per
 // workgroup and restage per chunk.
 #ifndef FLK_Q8_MM_RT
 #define FLK_Q8_MM_RT 4
@@ -379,8 +379,10 @@ constexpr int kMmTokenStride = 32 * kMmPad;  // floats per staged token
 #ifndef FLK_Q8_MM_ROW_TILES
 #define FLK_Q8_MM_ROW_TILES 8
 #endif
-// Row tiles one workgroup streams through its staged tokens (rows of one chunk).
+// Row tiles one workgroup streams through its staged tokens (rows of one
+// chunk), at most; fewer when the grid would otherwise leave CUs idle.
 constexpr uint32_t kMmRowTiles = FLK_Q8_MM_ROW_TILES;
+constexpr uint32_t kMmMinWorkgroups = 1024;  // 4 per CU
 
 // One block of RT rows (weights w0/w1, scales sc) against the staged tokens,
 // folded into acc[r][t] (q8_coop.wgsl:105-112 per output). Per word pair g,
@@ -618,7 +620,8 @@ __device__ __forceinline__ uint32_t q8_mm_rows(const Q8Args& a, uint32_t rt,
 // between them.
 template <int FUSE>
 __global__ __launch_bounds__(kQ8Threads, FLK_Q8_MM_WAVES1) void q8_mm1_kernel(Q8Args a,
-                                                                              uint32_t n_rg) {
+                                                                              uint32_t n_rg,
+                                                                              uint32_t rpw) {
   constexpr int RT = kMmRowsPerSlot, TT = kMmTokens;
   __shared__ __align__(16) float xs[TT * kMmTokenStride];
   __shared__ float s_scale[TT];
@@ -627,10 +630,10 @@ __global__ __launch_bounds__(kQ8Threads, FLK_Q8_MM_WAVES1) void q8_mm1_kernel(Q8
   const int q = threadIdx.x & 31;
   const uint32_t tok0 = tt * TT;
   const uint32_t n_rt = (a.n_rows + kMmRows - 1) / kMmRows;
-  const uint32_t rt_end = min(n_rt, (rg + 1) * kMmRowTiles);
+  const uint32_t rt_end = min(n_rt, (rg + 1) * rpw);
   q8_mm_stage<FUSE, FUSE == kMmNorm, TT>(a, 0, tok0, xs, s_scale);
   const bool live = (uint32_t)q < a.n_cols / 32;
-  for (uint32_t rt = rg * kMmRowTiles; rt < rt_end; rt++) {
+  for (uint32_t rt = rg * rpw; rt < rt_end; rt++) {
     const uint8_t* wrow[RT];
     const uint16_t* srow[RT];
     const uint32_t row0 = q8_mm_rows<RT>(a, rt, wrow, srow);
@@ -772,20 +775,29 @@ hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const flo
   const uint32_t n_rt = (n_rows + kMmRows - 1) / kMmRows;
   const uint32_t n_tt = (n_tokens + kMmTokens - 1) / kMmTokens;
   const bool one = n_cols <= (uint32_t)kMmChunkCols;
-  const uint32_t n_rg = one ? (n_rt + kMmRowTiles - 1) / kMmRowTiles : n_rt;
+  // Row tiles per workgroup (rows of one chunk): as many as keep the grid at
+  // kMmMinWorkgroups or more, up to kMmRowTiles.
+  uint32_t rpw = 1;
+  while (one && rpw < kMmRowTiles && (uint64_t)((n_rt + 2 * rpw - 1) / (2 * rpw)) * n_tt >=
+                                          kMmMinWorkgroups)
+    rpw *= 2;
+  const uint32_t n_rg = (n_rt + rpw - 1) / rpw;
   if (n_tokens >= FLK_Q8_MM_MIN_TOKENS && best_val == nullptr &&
       (uint64_t)n_rg * n_tt <= 0x7fffffffu) {
     gx = n_rg * n_tt;
     const int fuse = a.norm_gain != nullptr ? kMmNorm : (a.up != nullptr ? kMmSwiglu : kMmPlain);
+    auto go1 = [&](auto kernel) {
+      hipLaunchKernelGGL(kernel, dim3(gx), dim3(kQ8Threads), 0, st, a, n_rg, rpw);
+    };
     auto go = [&](auto kernel) {
       hipLaunchKernelGGL(kernel, dim3(gx), dim3(kQ8Threads), 0, st, a, n_rg);
     };
     if (fuse == kMmNorm)
-      one ? go(q8_mm1_kernel<kMmNorm>) : go(q8_mm_kernel<kMmNorm>);
+      one ? go1(q8_mm1_kernel<kMmNorm>) : go(q8_mm_kernel<kMmNorm>);
     else if (fuse == kMmSwiglu)
-      one ? go(q8_mm1_kernel<kMmSwiglu>) : go(q8_mm_kernel<kMmSwiglu>);
+      one ? go1(q8_mm1_kernel<kMmSwiglu>) : go(q8_mm_kernel<kMmSwiglu>);
     else
-      one ? go(q8_mm1_kernel<kMmPlain>) : go(q8_mm_kernel<kMmPlain>);
+      one ? go1(q8_mm1_kernel<kMmPlain>) : go(q8_mm_kernel<kMmPlain>);
   } else if (nb > (uint32_t)kQ8Lanes * kQ8MaxRegBlocks) {
     gx = (n_rows + 3) / 4 < 2048u ? (n_rows + 3) / 4 : 2048u;
     hipLaunchKernelGGL(q8_matvec_wide_kernel, dim3(gx, n_tokens), dim3(kQ8Threads), 0, st, a);

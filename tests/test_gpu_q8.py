@@ -79,6 +79,48 @@ def test_token_tiles_match_oracle(rng, rows, cols, n_tokens):
     assert np.array_equal(got, want), np.flatnonzero(got != want)[:8]
 
 
+@pytest.mark.parametrize("mode", ["plain", "norm", "gate_up"])
+def test_row_streaming_matches_small_batches(rng, mode):
+    """Large batches stream several row tiles through one staged token tile
+    (up to 8 at 1024 tokens x 4096 rows); they must equal the same tokens
+    projected 8 at a time (one row tile per workgroup), which the tests above
+    hold to the oracle -- and the first tokens are held to it here as well."""
+    rows, cols, n = 4096, 1024, 1024
+    packed = random_packed(rng, rows, cols)
+    w = ops.Q8Matrix.from_packed(packed, rows, cols)
+    x = rng.standard_normal(n * cols).astype(np.float32)
+    gain = rng.normal(1, 0.1, cols).astype(np.float32)
+    xb = ops.DeviceBuffer.from_array(x)
+    gb = ops.DeviceBuffer.from_array(gain)
+    n_out = rows // 2 if mode == "gate_up" else rows
+
+    def project(xbuf, ntok, out):
+        if mode == "plain":
+            ops.q8_matvec(w, xbuf, out, ntok)
+        elif mode == "norm":
+            ops.q8_matvec_ex(w, xbuf, out, ntok, norm_gain=gb, eps=oracle.QWEN3_EPS)
+        else:
+            ops.q8_gate_up_swiglu(w, xbuf, out, ntok, norm_gain=gb, eps=oracle.QWEN3_EPS)
+
+    big = ops.DeviceBuffer(n * n_out * 4)
+    project(xb, n, big)
+    small = ops.DeviceBuffer(8 * n_out * 4)
+    xs = ops.DeviceBuffer(8 * cols * 4)
+    got = big.download(n * n_out).reshape(n, n_out)
+    for t0 in range(0, n, 8):
+        xs.upload(x[t0 * cols:(t0 + 8) * cols])
+        project(xs, 8, small)
+        ops.sync()
+        assert np.array_equal(got[t0:t0 + 8], small.download(8 * n_out).reshape(8, n_out)), t0
+    xin = x[:8 * cols]
+    if mode != "plain":
+        xin = oracle.rmsnorm(xin, gain, cols, 8, oracle.QWEN3_EPS)
+    want = oracle.q8_matvec(packed, xin, rows, cols, 64, fused=True).reshape(8, rows)
+    if mode == "gate_up":  # rows 2i, 2i + 1 are a (gate, up) pair
+        want = oracle.swiglu(want[:, 0::2].ravel(), want[:, 1::2].ravel()).reshape(8, n_out)
+    assert np.array_equal(got[:8], want)
+
+
 def random_packed(rng, rows, cols):
     """Q8_0 bytes with random int8 quants and f16 scales around 4e-4 (what
     quantRowQ8 gives for N(0, 0.05) weights), built without the quantizer."""
