@@ -155,6 +155,50 @@ def test_matvec_coop_order_is_the_lane_tree():
     assert oracle.q8_matvec(packed, x, 1, cols, 0)[0] == 1.0
 
 
+def lane_tree(p):
+    """The reference's pairwise tree over 64 lane partials (strides 32 .. 1),
+    in f32 with the lower lane as the left operand; p is [64, ...]."""
+    p = np.array(p, np.float32)
+    for s in (32, 16, 8, 4, 2, 1):
+        p[:s] = p[:s] + p[s:2 * s]
+    return p[0]
+
+
+def recursive_halving(p64):
+    """What the tile kernels do with 64 leaf partials of 32 outputs: lane q
+    (of 32) adds leaf q + 32 to leaf q in place (the stride-32 step), then at
+    stride s = 16 .. 1 keeps the lower half of its value list when bit s of q
+    is clear (else the upper half moved down) and adds the copy its partner
+    q ^ s sends. Returns out[q] = the value lane q ends with."""
+    v = (p64[:32] + p64[32:]).astype(np.float32)     # [lane][output]
+    n = 32
+    for s in (16, 8, 4, 2, 1):
+        hi = (np.arange(32) & s) != 0
+        lo_half, up_half = v[:, :n // 2], v[:, n // 2:n]
+        keep = np.where(hi[:, None], up_half, lo_half)
+        send = np.where(hi[:, None], lo_half, up_half)
+        recv = send[np.arange(32) ^ s]
+        v = (keep + recv).astype(np.float32)
+        n //= 2
+    return v[:, 0]
+
+
+def test_recursive_halving_is_the_lane_tree():
+    # Partials with wildly different magnitudes make every rounding count: a
+    # wrong pairing or order would change the bits.
+    rng = np.random.default_rng(21)
+    for _ in range(20):
+        p = (rng.standard_normal((64, 32)) * 2.0 ** rng.integers(-20, 20, (64, 32))).astype(np.float32)
+        p[rng.random((64, 32)) < 0.2] = 0
+        want = lane_tree(p)
+        assert np.array_equal(recursive_halving(p), want)
+    # And the serial sum would differ somewhere (the check has teeth).
+    serial = np.zeros(32, np.float32)
+    for lane in range(64):
+        serial = (serial + p[lane]).astype(np.float32)
+    assert not np.array_equal(serial, want)
+
+
 def test_matvec_within_f32_bound_of_f64():
     rng = np.random.default_rng(11)
     rows, cols = 64, 3072
