@@ -525,7 +525,10 @@ static uint32_t keys_per_iter(const DecodeShape& s) {
 // kRaggedTargetWG workgroups, and each sequence gets ceil(blocks / bps).
 constexpr uint32_t kTargetWG = FLK_DECODE_TARGET_WG;
 constexpr uint32_t kRaggedTargetWG = FLK_DECODE_RAGGED_TARGET_WG;
-constexpr uint32_t kMinBps = 4;
+#ifndef FLK_DECODE_MIN_BPS
+#define FLK_DECODE_MIN_BPS 1
+#endif
+constexpr uint32_t kMinBps = FLK_DECODE_MIN_BPS;
 
 struct SplitPlan {
   uint32_t kpi, bps, max_splits;
