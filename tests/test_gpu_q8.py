@@ -79,13 +79,16 @@ def test_token_tiles_match_oracle(rng, rows, cols, n_tokens):
     assert np.array_equal(got, want), np.flatnonzero(got != want)[:8]
 
 
-@pytest.mark.parametrize("mode", ["plain", "norm", "gate_up"])
-def test_row_streaming_matches_small_batches(rng, mode):
+@pytest.mark.parametrize("mode,rows,n", [
+    ("plain", 4096, 1024), ("norm", 4096, 1024), ("gate_up", 4096, 1024),  # 8 row tiles
+    ("norm", 2050, 256), ("gate_up", 2050, 256),  # 2 row tiles, ragged last group and tile
+])
+def test_row_streaming_matches_small_batches(rng, mode, rows, n):
     """Large batches stream several row tiles through one staged token tile
-    (up to 8 at 1024 tokens x 4096 rows); they must equal the same tokens
-    projected 8 at a time (one row tile per workgroup), which the tests above
-    hold to the oracle -- and the first tokens are held to it here as well."""
-    rows, cols, n = 4096, 1024, 1024
+    (8 at 1024 tokens x 4096 rows, 2 at 256 x 2050); they must equal the same
+    tokens projected 8 at a time (one row tile per workgroup), which the tests
+    above hold to the oracle -- and the first tokens are held to it here too."""
+    cols = 1024
     packed = random_packed(rng, rows, cols)
     w = ops.Q8Matrix.from_packed(packed, rows, cols)
     x = rng.standard_normal(n * cols).astype(np.float32)
