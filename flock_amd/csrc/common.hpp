@@ -38,6 +38,8 @@ __device__ __forceinline__ float dpp(float v) {
 }
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
+constexpr int kDppRor4 = 0x124;       // row_ror:4, lane i <- (i + 4) mod 16 within its row
+constexpr int kDppRor8 = 0x128;       // row_ror:8, lane i <- i ^ 8 within its row
 constexpr int kDppHalfMirror = 0x141; // lane i <- 7 - i within 8
 constexpr int kDppMirror = 0x140;     // lane i <- 15 - i within 16
 
@@ -66,12 +68,27 @@ __device__ __forceinline__ float group_sum(float v) {
 // tree with strides 64, 32, ..., 1. Stride 64 is in-lane; the rest is an xor
 // butterfly, after which every lane holds the tree total (each level's value
 // in lane i equals tree[i mod stride], and addition is commutative).
+//
+// tree_sum64 is that butterfly (strides 32, 16, ..., 1, every lane adding its
+// partner i ^ stride) with the in-row strides on DPP: 8 is row_ror:8 (exactly
+// i ^ 8); 4 is row_ror:4, which reads lane (i + 4) mod 16 -- that is i ^ 4
+// or (i ^ 4) ^ 8, and after the stride-8 step lanes j and j ^ 8 hold the same
+// float (a + b and b + a), so it is the same value; 2 and 1 are quad_perm.
+__device__ __forceinline__ float tree_sum64(float p) {
+  p = p + shfl_xor(p, 32);
+  p = p + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, p), 0x401F));
+  p = p + dpp<kDppRor8>(p);
+  p = p + dpp<kDppRor4>(p);
+  p = p + dpp<kDppXor2>(p);
+  p = p + dpp<kDppXor1>(p);
+  return p;
+}
+
 template <int D>
 __device__ __forceinline__ void head_rmsnorm(float& e0, float& e1, float g0, float g1, float eps) {
   float p = e0 * e0;
   if (D == 128) p = p + e1 * e1;
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) p = p + shfl_xor(p, m);
+  p = tree_sum64(p);
   // rmsnorm.wgsl:68 with the reference's rounding: fr(fr(sum / n) + eps), then
   // 1/sqrt as one rounding (ops_ref.ts:39-45).
   const float mean = p / (float)D;

@@ -166,6 +166,19 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
 
   for (uint32_t base = wave; base < per_tok; base += kWaves * kBatch) {
     if (base != (uint32_t)wave) load_batch(base);
+    // The batch's norm scales (head_rmsnorm's arithmetic): every vector's
+    // sum of squares by the tree, then lane b evaluates vector b's
+    // 1 / sqrt(mean + eps) -- one f64 sequence for the batch instead of one
+    // per vector -- and each vector reads its scale back from lane b.
+    float mine = 0.f;
+#pragma unroll
+    for (int b = 0; b < kBatch; b++) {
+      float p = e0[b] * e0[b];
+      if (D == 128) p = p + e1[b] * e1[b];
+      p = tree_sum64(p);
+      mine = (lane & (kBatch - 1)) == b ? p : mine;
+    }
+    const float scale_mine = rsqrt_once(mine / (float)D + eps);
 #pragma unroll
     for (int b = 0; b < kBatch; b++) {
       const uint32_t idx = base + kWaves * b;
@@ -177,7 +190,10 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
       float x0 = e0[b], x1 = e1[b];
       if (g != nullptr) {  // uniform per wave
         const bool is_q = idx < n_heads;
-        head_rmsnorm<D>(x0, x1, is_q ? gq0 : gk0, is_q ? gq1 : gk1, eps);
+        const float scale =
+            __builtin_bit_cast(float, __builtin_amdgcn_readlane(__builtin_bit_cast(int, scale_mine), b));
+        x0 = (x0 * scale) * (is_q ? gq0 : gk0);
+        if (D == 128) x1 = (x1 * scale) * (is_q ? gq1 : gk1);
         head_rope<D>(x0, x1, s_cs, pairing, lane);
       }
       dst[lane] = x0;
