@@ -825,7 +825,7 @@ def main():
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
-        print(f"bench.py measures one GPU (asked for --gpus {args.gpus}): this build's attention "
+        print(f"bench.py measures one GPU (asked for --gpus {args.gpus}): flock_amd's attention "
               "path runs on a single MI355X and has no multi-GPU mode. Run with --gpus 1.",
               file=sys.stderr)
         sys.exit(2)
