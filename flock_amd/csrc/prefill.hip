@@ -208,24 +208,30 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     }
 
     // ---- S^T = K Q^T ------------------------------------------------------------
+    // Each MFMA depends on the previous one of its block's chain, so the
+    // blocks' chains are issued interleaved, step by step.
     floatx4 sacc[kHalfKB];
+    {
+      float kf[kHalfKB][DS];
 #pragma unroll
-    for (int b = 0; b < kHalfKB; b++) {
-      const int kb = half * kHalfKB + b;
-      float kf[DS];
-      const float* kr = &kt_lds[(kb * 16 + lc) * LDK + DS * lg];
+      for (int b = 0; b < kHalfKB; b++) {
+        const float* kr = &kt_lds[((half * kHalfKB + b) * 16 + lc) * LDK + DS * lg];
 #pragma unroll
-      for (int s4 = 0; s4 < DS / 4; s4++) {
-        const float4 v = *reinterpret_cast<const float4*>(kr + 4 * s4);
-        kf[4 * s4 + 0] = v.x;
-        kf[4 * s4 + 1] = v.y;
-        kf[4 * s4 + 2] = v.z;
-        kf[4 * s4 + 3] = v.w;
+        for (int s4 = 0; s4 < DS / 4; s4++) {
+          const float4 v = *reinterpret_cast<const float4*>(kr + 4 * s4);
+          kf[b][4 * s4 + 0] = v.x;
+          kf[b][4 * s4 + 1] = v.y;
+          kf[b][4 * s4 + 2] = v.z;
+          kf[b][4 * s4 + 3] = v.w;
+        }
       }
-      floatx4 c = {0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-      for (int s = 0; s < DS; s++) c = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[s], qreg[s], c, 0, 0, 0);
-      sacc[b] = c;
+      for (int b = 0; b < kHalfKB; b++) sacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+#pragma unroll
+      for (int s = 0; s < DS; s++)
+#pragma unroll
+        for (int b = 0; b < kHalfKB; b++)
+          sacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[b][s], qreg[s], sacc[b], 0, 0, 0);
     }
 
     // ---- online softmax of this lane's row (base 2) ----------------------------
