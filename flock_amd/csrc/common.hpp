@@ -38,10 +38,46 @@ __device__ __forceinline__ float dpp(float v) {
 }
 constexpr int kDppXor1 = 0xB1;        // quad_perm [1,0,3,2]
 constexpr int kDppXor2 = 0x4E;        // quad_perm [2,3,0,1]
-constexpr int kDppRor4 = 0x124;       // row_ror:4, lane i <- (i + 4) mod 16 within its row
+constexpr int kDppRor4 = 0x124;       // row_ror:4, lane i <- (i - 4) mod 16 within its row
 constexpr int kDppRor8 = 0x128;       // row_ror:8, lane i <- i ^ 8 within its row
+constexpr int kDppRor12 = 0x12C;      // row_ror:12, lane i <- (i + 4) mod 16 within its row
 constexpr int kDppHalfMirror = 0x141; // lane i <- 7 - i within 8
 constexpr int kDppMirror = 0x140;     // lane i <- 15 - i within 16
+
+// v of lane i ^ M, for M = 1, 2, 4, 8, 16 without LDS traffic: quad_perm for
+// 1 and 2, row_ror:8 (exactly i ^ 8) for 8, row_ror:12 or :4 for 4 (lane i
+// with bit 2 clear reads i + 4, with it set i - 4), ds_swizzle for 16.
+// (row_ror:n hands lane i the value of lane (i - n) mod 16 of its row.)
+template <int M>
+__device__ __forceinline__ float xor_lane(float v) {
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16, "xor_lane");
+  if constexpr (M == 1) {
+    return dpp<kDppXor1>(v);
+  } else if constexpr (M == 2) {
+    return dpp<kDppXor2>(v);
+  } else if constexpr (M == 8) {
+    return dpp<kDppRor8>(v);
+  } else if constexpr (M == 4) {
+    const float up = dpp<kDppRor12>(v), down = dpp<kDppRor4>(v);  // lanes i + 4, i - 4
+    return (threadIdx.x & 4) ? down : up;
+  } else {
+    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
+  }
+}
+
+// The pairwise tree over P lanes (P a power of two <= 64) as an xor
+// butterfly, strides P/2 .. 1: every lane of an aligned group of P ends with
+// the group's tree total.
+template <int P>
+__device__ __forceinline__ float lane_tree(float v) {
+  if constexpr (P >= 64) v = v + shfl_xor(v, 32);
+  if constexpr (P >= 32) v = v + xor_lane<16>(v);
+  if constexpr (P >= 16) v = v + xor_lane<8>(v);
+  if constexpr (P >= 8) v = v + xor_lane<4>(v);
+  if constexpr (P >= 4) v = v + xor_lane<2>(v);
+  if constexpr (P >= 2) v = v + xor_lane<1>(v);
+  return v;
+}
 
 // Sum over aligned groups of `width` lanes (a power of two <= 64); every lane
 // of a group ends with the same total (each step adds a pair of equal-shaped
@@ -71,7 +107,7 @@ __device__ __forceinline__ float group_sum(float v) {
 //
 // tree_sum64 is that butterfly (strides 32, 16, ..., 1, every lane adding its
 // partner i ^ stride) with the in-row strides on DPP: 8 is row_ror:8 (exactly
-// i ^ 8); 4 is row_ror:4, which reads lane (i + 4) mod 16 -- that is i ^ 4
+// i ^ 8); 4 is row_ror:4, which reads lane (i - 4) mod 16 -- that is i ^ 4
 // or (i ^ 4) ^ 8, and after the stride-8 step lanes j and j ^ 8 hold the same
 // float (a + b and b + a), so it is the same value; 2 and 1 are quad_perm.
 __device__ __forceinline__ float tree_sum64(float p) {

@@ -138,9 +138,7 @@ __device__ __forceinline__ float q8_rms_scale(uint32_t n, float eps, LOAD ld) {
       p1 = fma32(v[k + 1], v[k + 1], p1);
     }
   }
-  float sum = p0 + p1;
-#pragma unroll
-  for (int m = 32; m >= 1; m >>= 1) sum += shfl_xor(sum, m);
+  const float sum = tree_sum64(p0 + p1);
   const float mean = sum / (float)n;
   return rsqrt_once(mean + eps);
 }
@@ -274,8 +272,7 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
       for (int j = 0; j < NB; j++)
         if (live[j]) part = q8_block(part, q8_scale(hs[u][j]), w0[u][j], w1[u][j], xr[j]);
       // The reference's tree over 64 partials; strides >= P add exact zeros.
-#pragma unroll
-      for (int m = P / 2; m >= 1; m >>= 1) part += shfl_xor(part, m);
+      part = lane_tree<P>(part);
       const uint32_t row = (g0 + waves * u) * R + sub;
       if (R >= 2 && a.act != nullptr) {  // uniform: (gate, up) row pairs -> SwiGLU
         const float up = shfl_xor(part, R >= 2 ? P : 0);  // the odd row of the pair
@@ -330,8 +327,7 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
       }
       part = q8_block(part, q8_scale(a.scales[(size_t)row * nb + b]), src[0], src[1], xb);
     }
-#pragma unroll
-    for (int m = 32; m >= 1; m >>= 1) part += shfl_xor(part, m);
+    part = lane_tree<64>(part);
     if (lane == 0) {
       const size_t oi = (size_t)tok * a.n_rows + row;
       if (a.res != nullptr) part = a.res[oi] + part;
@@ -555,7 +551,7 @@ template <int S, int N, int I = 0>
 __device__ __forceinline__ void q8_halve_step(float (&v)[32], bool hi) {
   if constexpr (I < N / 2) {
     const float lo = v[I], up = v[I + N / 2];
-    v[I] = (hi ? up : lo) + shfl_xor(hi ? lo : up, S);
+    v[I] = (hi ? up : lo) + xor_lane<S>(hi ? lo : up);
     q8_halve_step<S, N, I + 1>(v, hi);
   }
 }
@@ -587,7 +583,7 @@ __device__ __forceinline__ void q8_mm_finish(const Q8Args& a, const float (&acc)
   const uint32_t tok = tok0 + q / RT, row = row0 + q % RT;
   float out = v[0];
   if (a.act != nullptr) {  // (gate, up) row pairs: lanes q, q ^ 1 (row0 is a multiple of 4)
-    const float up = shfl_xor(out, 1);
+    const float up = xor_lane<1>(out);
     if ((q & 1) == 0 && tok < a.n_tokens && row + 1 < a.n_rows)
       a.act[(size_t)tok * (a.n_rows / 2) + row / 2] = q8_swiglu(out, up);
   } else if (tok < a.n_tokens && row < a.n_rows) {
