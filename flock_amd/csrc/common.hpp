@@ -73,7 +73,10 @@ __device__ __forceinline__ float lane_tree(float v) {
   if constexpr (P >= 64) v = v + shfl_xor(v, 32);
   if constexpr (P >= 32) v = v + xor_lane<16>(v);
   if constexpr (P >= 16) v = v + xor_lane<8>(v);
-  if constexpr (P >= 8) v = v + xor_lane<4>(v);
+  // After the stride-8 step lanes j and j ^ 8 hold the same float, so one
+  // row_ror:4 (lane i - 4, i.e. i ^ 4 or (i ^ 4) ^ 8) serves as xor 4.
+  if constexpr (P >= 16) v = v + dpp<kDppRor4>(v);
+  else if constexpr (P >= 8) v = v + xor_lane<4>(v);
   if constexpr (P >= 4) v = v + xor_lane<2>(v);
   if constexpr (P >= 2) v = v + xor_lane<1>(v);
   return v;

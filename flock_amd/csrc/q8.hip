@@ -51,6 +51,7 @@ constexpr int kQ8Threads = 256;   // 4 waves
 template <int NB>
 constexpr int q8_unroll() { return NB == 1 ? FLK_Q8_UNROLL : (NB == 2 ? 2 : 1); }
 constexpr int kQ8MaxRegBlocks = 4;  // x blocks per lane kept in registers (8192 columns)
+constexpr uint32_t kQ8LdsTreeRows = 65536;  // rows from which the lane tree uses the LDS unit
 
 struct Q8Args {
   const uint8_t* qs;
@@ -209,7 +210,10 @@ __device__ __forceinline__ void q8_load_rows(const Q8Args& a, uint32_t g0, uint3
 // P logical lanes per row, NB x blocks per lane in registers (NB * 64 >= the
 // row's block count). Grid: (workgroups over row groups, tokens).
 // FUSE: the input fusions (rmsnorm / swiglu) are compiled in.
-template <int P, int NB, bool FUSE>
+// LDS_TREE: the lane tree's exchanges through ds_bpermute (the LDS unit)
+// instead of DPP (the VALU): for very tall matrices (the LM head), where the
+// VALU is the busier unit and latency is hidden by many row groups.
+template <int P, int NB, bool FUSE, bool LDS_TREE = false>
 __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
   constexpr int R = kWave / P;  // rows per wave per step
   constexpr int kQ8Unroll = q8_unroll<NB>();
@@ -272,7 +276,12 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
       for (int j = 0; j < NB; j++)
         if (live[j]) part = q8_block(part, q8_scale(hs[u][j]), w0[u][j], w1[u][j], xr[j]);
       // The reference's tree over 64 partials; strides >= P add exact zeros.
-      part = lane_tree<P>(part);
+      if (LDS_TREE) {
+#pragma unroll
+        for (int m = P / 2; m >= 1; m >>= 1) part = part + shfl_xor(part, m);
+      } else {
+        part = lane_tree<P>(part);
+      }
       const uint32_t row = (g0 + waves * u) * R + sub;
       if (R >= 2 && a.act != nullptr) {  // uniform: (gate, up) row pairs -> SwiGLU
         const float up = shfl_xor(part, R >= 2 ? P : 0);  // the odd row of the pair
@@ -700,13 +709,14 @@ __global__ __launch_bounds__(kQ8Threads, FLK_Q8_MM_WAVES) void q8_mm_kernel(Q8Ar
 // Workgroups: one resident wave of them (every CU filled to its occupancy
 // limit, so no workgroup waits for another to finish), never more than there
 // are row groups.
-template <int P, int NB, bool FUSE>
+template <int P, int NB, bool FUSE, bool LDS_TREE = false>
 static uint32_t q8_grid_x(uint32_t n_groups) {
   static int per_cu = 0;
   if (per_cu == 0) {
     int n = 0;
     if (FLK_Q8_WG_PER_CU > 0 ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, q8_matvec_kernel<P, NB, FUSE>, kQ8Threads, 0) !=
+        hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, q8_matvec_kernel<P, NB, FUSE, LDS_TREE>, kQ8Threads, 0) !=
             hipSuccess ||
         n < 1)
       n = FLK_Q8_WG_PER_CU > 0 ? FLK_Q8_WG_PER_CU : 2;
@@ -733,6 +743,12 @@ static uint32_t launch_q8(const Q8Args& a, hipStream_t st) {
     const uint32_t gx = q8_grid_x<P, NB, true>(groups);
     hipLaunchKernelGGL((q8_matvec_kernel<P, NB, true>), dim3(gx, a.n_tokens), dim3(kQ8Threads), 0,
                        st, a);
+    return gx;
+  }
+  if (a.n_rows >= kQ8LdsTreeRows) {
+    const uint32_t gx = q8_grid_x<P, NB, false, true>(groups);
+    hipLaunchKernelGGL((q8_matvec_kernel<P, NB, false, true>), dim3(gx, a.n_tokens),
+                       dim3(kQ8Threads), 0, st, a);
     return gx;
   }
   const uint32_t gx = q8_grid_x<P, NB, false>(groups);
