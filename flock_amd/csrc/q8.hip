@@ -370,13 +370,10 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
 // Weights come straight from memory. Rows of one chunk (q/k/v, gate/up at
 // hidden 1024) stage their token tile once per workgroup -- rmsnorm scales
 // included, computed from the staged rows -- and stream up to kMmRowTiles row
-// tiles// through it with no barrier in between; longer rows take one tile per
+// tiles through it with no barrier in between; longer rows take one tile per
 // workgroup and restage per chunk.
-#ifndef FLK_Q8_MM_RT
-#define FLK_Q8_MM_RT 4
-#endif
-constexpr int kMmRowsPerSlot = FLK_Q8_MM_RT;
-constexpr int kMmTokens = 32 / FLK_Q8_MM_RT;  // 32 outputs per lane
+constexpr int kMmRowsPerSlot = 4;
+constexpr int kMmTokens = 8;  // 4 x 8 = 32 outputs per lane
 constexpr int kMmRows = (kQ8Threads / kWave) * 2 * kMmRowsPerSlot;  // 32
 constexpr int kMmPad = 36;
 constexpr int kMmChunkCols = 1024;
