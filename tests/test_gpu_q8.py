@@ -124,6 +124,50 @@ def test_row_streaming_matches_small_batches(rng, mode, rows, n):
     assert np.array_equal(got[:8], want)
 
 
+def test_tile_kernels_equal_per_token_kernel_on_random_shapes():
+    """Seeded random shapes and fusions: a batch of >= 8 tokens (tile kernels,
+    any row tiling) equals the same tokens projected at most 7 at a time (the
+    per-token kernel), bit for bit."""
+    rng = np.random.default_rng(2024)
+    for case in range(24):
+        rows = int(rng.integers(1, 2600))
+        cols = 32 * int(rng.integers(1, 130))
+        n = int(rng.integers(8, 300))
+        fuse = ["plain", "norm", "up", "res", "gate_up"][case % 5]
+        if fuse == "gate_up":
+            rows += rows % 2
+            cols = min(cols, 1024)
+        packed = random_packed(rng, rows, cols)
+        w = ops.Q8Matrix.from_packed(packed, rows, cols)
+        x = rng.standard_normal(n * cols).astype(np.float32)
+        aux = rng.standard_normal(n * max(rows, cols)).astype(np.float32)
+        gain = ops.DeviceBuffer.from_array(rng.normal(1, 0.1, cols).astype(np.float32))
+        n_out = rows // 2 if fuse == "gate_up" else rows
+
+        def run(t0, t1):
+            k = t1 - t0
+            xb = ops.DeviceBuffer.from_array(x[t0 * cols:t1 * cols])
+            ob = ops.DeviceBuffer(k * n_out * 4)
+            if fuse == "plain":
+                ops.q8_matvec(w, xb, ob, k)
+            elif fuse == "norm":
+                ops.q8_matvec_ex(w, xb, ob, k, norm_gain=gain, eps=oracle.QWEN3_EPS)
+            elif fuse == "up":
+                ub = ops.DeviceBuffer.from_array(aux[t0 * cols:t1 * cols])
+                ops.q8_matvec_ex(w, xb, ob, k, up=ub)
+            elif fuse == "res":
+                rb = ops.DeviceBuffer.from_array(aux[t0 * rows:t1 * rows])
+                ops.q8_matvec_ex(w, xb, ob, k, res=rb)
+            else:
+                ops.q8_gate_up_swiglu(w, xb, ob, k, norm_gain=gain, eps=oracle.QWEN3_EPS)
+            ops.sync()
+            return ob.download(k * n_out)
+
+        big = run(0, n)
+        small = np.concatenate([run(t, min(t + 7, n)) for t in range(0, n, 7)])
+        assert np.array_equal(big, small), (case, rows, cols, n, fuse)
+
+
 def random_packed(rng, rows, cols):
     """Q8_0 bytes with random int8 quants and f16 scales around 4e-4 (what
     quantRowQ8 gives for N(0, 0.05) weights), built without the quantizer."""
