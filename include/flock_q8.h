@@ -56,8 +56,8 @@ int32_t flk_q8_matvec_ex(const int8_t* qs, const uint16_t* scales, const float* 
  * two matvecs and an elementwise dispatch): the weights are 2 * n_ffn rows
  * with gate and up INTERLEAVED (row 2i = ffn_gate row i, row 2i + 1 = ffn_up
  * row i; interleave at upload), and act[t][i] = swiglu(gate_i, up_i) as
- * flk_swiglu computes it. norm_gain (optional) RMS-normalises x first, as in
- * flk_q8_matvec_ex. n_cols <= 1024 (two or more rows per wave). */
+ * flk_swiglu computes it. norm_gain (optional, 16-byte aligned) RMS-normalises
+ * x first, as in flk_q8_matvec_ex. n_cols <= 1024 (two or more rows per wave). */
 int32_t flk_q8_gate_up_swiglu(const int8_t* qs, const uint16_t* scales, const float* x,
                               float* act, uint32_t n_ffn, uint32_t n_cols, uint32_t n_tokens,
                               const float* norm_gain, float norm_eps);
