@@ -39,6 +39,8 @@ of the hot path over one batch of synthetic, HBM-resident input:
              tile kernel). TFLOP/s against the fp32 vector peak.
   prompt2k   Time to first token: a 2048-token prompt through Model.step
              (28 layers in prefill + head). tokens/s and ms per prompt.
+  replay32k  Chunked replay: a 64-id chunk at position 32768 through Model.step
+             (28 layers of prefill onto the cache + head). tokens/s.
 
 The default run also measures prefill2k (the metric's second half) and reports
 it under "prefill", the LM-head projection under "q8_lm_head", whole-model
@@ -105,6 +107,8 @@ class Workload:
     unit = "GB/s"
     bound = "hbm"
     calls_per_step = 1
+    data = ("synthetic: seeded N(0,1) q/k/v and K/V caches, norm gains N(1,0.1); no weights "
+            "(attention path only)")
 
     def value(self, ms):
         scale = 1e9 if self.unit == "GB/s" else 1e12
@@ -357,6 +361,7 @@ class Ragged(Workload):
 
 class Copy(Workload):
     name = "copy"
+    data = "synthetic: a 1 GiB N(0,1) buffer"
     kernel = "torch Tensor.copy_ (device to device)"
 
     def __init__(self, torch, ops, nbytes=1 << 30):
@@ -377,6 +382,9 @@ class Copy(Workload):
 
 class Q8LmHead(Workload):
     """Qwen3-0.6B's tied LM head as one Q8_0 matvec: 151936 x 1024."""
+
+    data = ("synthetic: random Q8_0 weights of the Qwen3-0.6B shapes (seeded quants, f16 "
+            "scales), seeded N(0,1) inputs, zeroed or seeded caches")
 
     name = "q8lmhead"
     kernel = "flk_q8_matvec: q8_matvec_kernel<32,1> (coop(64) order, 2 rows per wave)"
@@ -439,6 +447,9 @@ class Q8Proj(Workload):
     28 layers: q 2048x1024, k and v 1024x1024, o 1024x2048, gate and up
     3072x1024, down 1024x3072."""
 
+    data = ("synthetic: random Q8_0 weights of the Qwen3-0.6B shapes (seeded quants, f16 "
+            "scales), seeded N(0,1) inputs, zeroed or seeded caches")
+
     name = "q8proj"
     kernel = "flk_q8_matvec (7 calls per layer; mean over the calls)"
     shapes = [(2048, 1024), (1024, 1024), (1024, 1024), (1024, 2048), (3072, 1024),
@@ -494,6 +505,9 @@ class Q8Prefill(Workload):
     kernel (q8_mm_kernel), exact to the coop(64) order. VALU-bound: the
     exact summation order rules out MFMA."""
 
+    data = ("synthetic: random Q8_0 weights of the Qwen3-0.6B shapes (seeded quants, f16 "
+            "scales), seeded N(0,1) inputs, zeroed or seeded caches")
+
     name = "q8prefill"
     unit = "TFLOP/s"
     bound = "valu"
@@ -533,6 +547,9 @@ class Prompt2k(Workload):
     (embedding, 28 Qwen3-0.6B layers in prefill -- Q8_0 tile projections with
     fused norms and SwiGLU, q/k norm + RoPE + K/V write, fp32-MFMA causal
     attention -- then the head and argmax on the last row, read back)."""
+
+    data = ("synthetic: random Q8_0 weights of the Qwen3-0.6B shapes (seeded quants, f16 "
+            "scales), seeded N(0,1) inputs, zeroed or seeded caches")
 
     name = "prompt2k"
     unit = "tokens/s"
@@ -586,11 +603,72 @@ class Prompt2k(Workload):
                 "flops_per_prompt": self.work_per_call}
 
 
+class Replay32k(Prompt2k):
+    """Chunked replay through the whole model (FLOCK_REPLAY_CHUNK = 64): a
+    64-id chunk appended at position 32768 onto a 32768-key cache by
+    Model.step -- 28 layers of prefill (Q8_0 tile projections, chunk
+    attention over the cache with split keys) + head. The caches are zeroed
+    once; each step rewinds to position 32768."""
+
+    name = "replay32k"
+    kernel = "Model.step(64 ids at position 32768): embed, 28 x encodePrefill, lm_head"
+    n_tokens = 64
+    n_keys = 32768
+
+    def __init__(self, torch, ops):
+        from flock_amd.decoder import DecoderConfig
+        from flock_amd.model import Model
+        self.torch, self.ops = torch, ops
+        rng = np.random.default_rng(31)
+        cfg = DecoderConfig(maxKeys=self.n_keys + self.n_tokens, maxPrefill=self.n_tokens)
+        log(f"[{self.name}] building the model (random Q8_0 weights)")
+        layers = []
+        for _ in range(28):
+            w = {n: random_q8(rng, r, c) for n, (r, c) in cfg.shapes().items()}
+            for n, sz in (("attn_norm.weight", cfg.hidden), ("ffn_norm.weight", cfg.hidden),
+                          ("attn_q_norm.weight", cfg.headDim), ("attn_k_norm.weight", cfg.headDim)):
+                w[n] = (1 + 0.1 * rng.standard_normal(sz)).astype(np.float32)
+            layers.append(w)
+        self.vocab = 151936
+        self.model = Model(cfg, layers, random_q8(rng, self.vocab, cfg.hidden, 0.02),
+                           (1 + 0.1 * rng.standard_normal(cfg.hidden)).astype(np.float32),
+                           self.vocab, max_generate=1)
+        del layers
+        for layer in self.model.layers:
+            layer.buf["kcache"].zero()
+            layer.buf["vcache"].zero()
+        self.ids = rng.integers(0, self.vocab, self.n_tokens).astype(np.uint32)
+        macs = sum(r * c for r, c in cfg.shapes().values())
+        n, H, d = self.n_tokens, cfg.nHeads, cfg.headDim
+        attn = 4 * H * d * sum(self.n_keys + i + 1 for i in range(n))  # QK^T and PV, causal
+        self.work_per_call = 28 * (2 * macs * n + attn) + 2 * self.vocab * cfg.hidden
+        self.work_per_step = self.work_per_call
+
+    def call(self, i=0):
+        m = self.model
+        m.nKeys = self.n_keys
+        for layer in m.layers:
+            layer.nKeys = self.n_keys
+        m.step(self.ids)
+
+    def extra(self, ms):
+        return {"ms_per_chunk": round(ms, 3)}
+
+    def config(self):
+        return {"workload": "chunked replay: a 64-id chunk at position 32768 through 28 "
+                            "Qwen3-0.6B layers (prefill onto a 32768-key cache) + head",
+                "layers": 28, "tokens": self.n_tokens, "n_keys": self.n_keys,
+                "vocab": self.vocab, "flops_per_chunk": self.work_per_call}
+
+
 class Token(Workload):
     """One greedy decode token through all 28 Qwen3-0.6B layers and the head:
     per layer the five DecoderLayer calls (fused projections + the attention
     slice), then flk_lm_head (output norm, tied 151936 x 1024 projection,
     argmax). Random Q8_0 weights, zeroed caches at position n_keys - 1."""
+
+    data = ("synthetic: random Q8_0 weights of the Qwen3-0.6B shapes (seeded quants, f16 "
+            "scales), seeded N(0,1) inputs, zeroed or seeded caches")
 
     unit = "GB/s"
     kernel = ("DecoderLayer.encode x 28 + flk_lm_head (q8_matvec_kernel, decode_split/merge, "
@@ -673,6 +751,9 @@ class Gen(Workload):
     position, fed-back token and token log on the device. A step is 32 tokens
     decoded from position n_keys - 1 (the caches are rewound between steps)."""
 
+    data = ("synthetic: random Q8_0 weights of the Qwen3-0.6B shapes (seeded quants, f16 "
+            "scales), seeded N(0,1) inputs, zeroed or seeded caches")
+
     unit = "GB/s"
     kernel = "Model.replay: one hipGraphLaunch per token (embed, 28 x 6 kernels, head, advance)"
     n_keys = 32769
@@ -745,8 +826,8 @@ class Gen512(Gen):
 
 
 WORKLOADS = {c.name: c for c in (Decode32k, Prefill2k, Ragged, Chunk32k, Decode512, Copy,
-                                 Q8LmHead, Q8Proj, Q8Prefill, Prompt2k, Token32k, Token512,
-                                 Gen32k, Gen512)}
+                                 Q8LmHead, Q8Proj, Q8Prefill, Prompt2k, Replay32k, Token32k,
+                                 Token512, Gen32k, Gen512)}
 
 
 def settle_clocks(torch, w, seconds=0.5):
@@ -797,7 +878,7 @@ def run(torch, ops, stream, name, steps, warmup):
     log(f"[{name}] {ms:.3f} ms/step (host wall {wall_ms:.3f}), {value:.2f} {w.unit}; "
         f"dominant call {call_ms * 1e3:.2f} us")
     out = {"value": round(value, 3), "unit": w.unit, "ms_per_step": round(ms, 4),
-           "config": w.config(),
+           "data": w.data, "config": w.config(),
            "roofline": w.roofline(call_ms, traffic_from_profiles(f"{name}_pmc.md"))}
     if hasattr(w, "extra"):
         out.update(w.extra(ms))
@@ -844,8 +925,7 @@ def main():
                "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
                "ms_per_step": main_res["ms_per_step"], "higher_is_better": True,
                "scaling": "weak", "vs_baseline": None, "dtype": "f32",
-               "data": "synthetic: seeded N(0,1) q/k/v and K/V caches, norm gains N(1,0.1); "
-                       "no weights (attention path only)",
+               "data": main_res["data"],
                "config": main_res["config"], "roofline": main_res["roofline"]}
         for k in ("tokens_per_s", "ms_per_token"):
             if k in main_res:
@@ -856,8 +936,9 @@ def main():
             out["frac_of_fp32_mfma_peak"] = round(main_res["value"] / FP32_MFMA_PEAK_TFLOPS, 4)
         elif main_res["unit"] == "TFLOP/s":
             out["frac_of_fp32_vector_peak"] = round(main_res["value"] / FP32_VECTOR_PEAK_TFLOPS, 4)
-        if "ms_per_prompt" in main_res:
-            out["ms_per_prompt"] = main_res["ms_per_prompt"]
+        for k in ("ms_per_prompt", "ms_per_chunk"):
+            if k in main_res:
+                out[k] = main_res[k]
         pre_cpu = q8_cpu = None
         if args.workload == "decode32k" and not args.no_secondary:
             p, pre_cpu = run(torch, ops, stream, "prefill2k", max(5, args.steps), args.warmup)
