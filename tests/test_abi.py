@@ -40,6 +40,13 @@ def test_header_and_binding_agree():
     assert declared_functions() == set(_lib.SIGNATURES)
 
 
+def test_integration_binding_lists_every_declared_symbol():
+    """INTEGRATION.md's Deno.dlopen table names every entry point, no more."""
+    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
+    bound = set(re.findall(r"\b(flk_\w+):\s*\{\s*parameters", text))
+    assert bound == declared_functions(), (declared_functions() - bound, bound - declared_functions())
+
+
 def test_library_exports_every_declared_symbol():
     L = _lib.lib()
     for name in declared_functions():
