@@ -388,9 +388,7 @@ constexpr uint32_t kMmMinWorkgroups = 1024;  // 4 per CU
 
 // One block of RT rows (weights w0/w1, scales sc) against the staged tokens,
 // folded into acc[r][t] (q8_coop.wgsl:105-112 per output). Per word pair g,
-// the quants of every row are converted once and used for every token (more
-// tokens than rows), or the x of every token is loaded once and used for
-// every row (more rows than tokens).
+// the quants of every row are converted once and used for every token.
 template <int RT, int TT>
 __device__ __forceinline__ void q8_mm_block(float (&acc)[RT][TT], const uint4 (&w0)[RT],
                                             const uint4 (&w1)[RT], const float (&sc)[RT],
@@ -417,31 +415,16 @@ __device__ __forceinline__ void q8_mm_block(float (&acc)[RT][TT], const uint4 (&
       d1 = __builtin_fmaf(qf[7], xc.w, d1);
       acc[r][t] = __builtin_fmaf(sc[r], d0 + d1, acc[r][t]);
     };
-    if constexpr (TT >= RT) {
-      float qf[RT][8];
+    static_assert(TT >= RT, "quants are converted once per row and used for every token");
+    float qf[RT][8];
 #pragma unroll
-      for (int r = 0; r < RT; r++) quants(r, qf[r]);
+    for (int r = 0; r < RT; r++) quants(r, qf[r]);
 #pragma unroll
-      for (int t = 0; t < TT; t++) {
-        const float4 xa = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g);
-        const float4 xc = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g + 4);
+    for (int t = 0; t < TT; t++) {
+      const float4 xa = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g);
+      const float4 xc = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g + 4);
 #pragma unroll
-        for (int r = 0; r < RT; r++) fold(r, t, qf[r], xa, xc);
-      }
-    } else {
-      float4 xa[TT], xc[TT];
-#pragma unroll
-      for (int t = 0; t < TT; t++) {
-        xa[t] = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g);
-        xc[t] = *reinterpret_cast<const float4*>(xb + t * kMmTokenStride + 8 * g + 4);
-      }
-#pragma unroll
-      for (int r = 0; r < RT; r++) {
-        float qf[8];
-        quants(r, qf);
-#pragma unroll
-        for (int t = 0; t < TT; t++) fold(r, t, qf, xa[t], xc[t]);
-      }
+      for (int r = 0; r < RT; r++) fold(r, t, qf[r], xa, xc);
     }
   }
 }
