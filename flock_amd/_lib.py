@@ -49,6 +49,11 @@ SIGNATURES: dict[str, tuple] = {
         _i32,
         [_p, _p, _p, _p, _p, _p, _f32, _i32, _p, _p, _p, _u32, _u32, _u32, _u32, _u32, _u32],
     ),
+    "flk_qk_prologue_strided": (
+        _i32,
+        [_p, _p, _p, _u32, _p, _p, _p, _f32, _i32, _p, _p, _p, _u32, _u32, _u32, _u32, _u32,
+         _u32],
+    ),
     "flk_attn_decode": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32, _u32, _p, _u64]),
     "flk_attn_prefill": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32, _p, _u64]),
     "flk_decode_layer": (

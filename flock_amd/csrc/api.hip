@@ -213,11 +213,12 @@ int32_t flk_kv_append(const float* kn, const float* v, float* kcache, float* vca
       "flk_kv_append");
 }
 
-int32_t flk_qk_prologue(const float* q_raw, const float* k_raw, const float* v_raw,
-                        const float* gq, const float* gk, const float* inv_freq, float eps,
-                        int32_t pairing, float* qn_out, float* kcache, float* vcache,
-                        uint32_t n_tokens, uint32_t pos0, uint32_t n_heads, uint32_t n_kv_heads,
-                        uint32_t head_dim, uint32_t max_keys) {
+static int32_t qk_prologue_common(const float* q_raw, const float* k_raw, const float* v_raw,
+                                  uint32_t in_stride, const float* gq, const float* gk,
+                                  const float* inv_freq, float eps, int32_t pairing, float* qn_out,
+                                  float* kcache, float* vcache, uint32_t n_tokens, uint32_t pos0,
+                                  uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                                  uint32_t max_keys, const char* what) {
   FLK_NONNULL(q_raw);
   FLK_NONNULL(k_raw);
   FLK_NONNULL(v_raw);
@@ -232,13 +233,37 @@ int32_t flk_qk_prologue(const float* q_raw, const float* k_raw, const float* v_r
   if (n_tokens == 0) return fail(FLK_ERR_ARG, "n_tokens must be >= 1, got 0");
   if (pairing != FLK_ROPE_NEOX && pairing != FLK_ROPE_NORM)
     return fail(FLK_ERR_ARG, "rope pairing %d (0 = neox, 1 = norm)", pairing);
+  if (in_stride != 0 && in_stride < n_heads * head_dim)
+    return fail(FLK_ERR_ARG, "in_stride %u is shorter than a q row (%u floats)", in_stride,
+                n_heads * head_dim);
   if ((uint64_t)pos0 + n_tokens > max_keys)
     return fail(FLK_ERR_CACHE_FULL, "KV cache would exceed %u keys (%u + %u)", max_keys, pos0,
                 n_tokens);
   return hip_status(launch_qk_prologue(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out,
                                        kcache, vcache, n_tokens, pos0, n_heads, n_kv_heads,
-                                       head_dim, g_stream),
-                    "flk_qk_prologue");
+                                       head_dim, g_stream, in_stride),
+                    what);
+}
+
+int32_t flk_qk_prologue(const float* q_raw, const float* k_raw, const float* v_raw,
+                        const float* gq, const float* gk, const float* inv_freq, float eps,
+                        int32_t pairing, float* qn_out, float* kcache, float* vcache,
+                        uint32_t n_tokens, uint32_t pos0, uint32_t n_heads, uint32_t n_kv_heads,
+                        uint32_t head_dim, uint32_t max_keys) {
+  return qk_prologue_common(q_raw, k_raw, v_raw, 0, gq, gk, inv_freq, eps, pairing, qn_out,
+                            kcache, vcache, n_tokens, pos0, n_heads, n_kv_heads, head_dim,
+                            max_keys, "flk_qk_prologue");
+}
+
+int32_t flk_qk_prologue_strided(const float* q_raw, const float* k_raw, const float* v_raw,
+                                uint32_t in_stride, const float* gq, const float* gk,
+                                const float* inv_freq, float eps, int32_t pairing,
+                                float* qn_out, float* kcache, float* vcache, uint32_t n_tokens,
+                                uint32_t pos0, uint32_t n_heads, uint32_t n_kv_heads,
+                                uint32_t head_dim, uint32_t max_keys) {
+  return qk_prologue_common(q_raw, k_raw, v_raw, in_stride, gq, gk, inv_freq, eps, pairing,
+                            qn_out, kcache, vcache, n_tokens, pos0, n_heads, n_kv_heads, head_dim,
+                            max_keys, "flk_qk_prologue_strided");
 }
 
 int32_t flk_attn_decode(const float* q, const float* kcache, const float* vcache, float* o,

@@ -200,7 +200,8 @@ hipError_t launch_qk_prologue(const float* q_raw, const float* k_raw, const floa
                               const float* gq, const float* gk, const float* inv_freq, float eps,
                               int32_t pairing, float* qn_out, float* kcache, float* vcache,
                               uint32_t n_tokens, uint32_t pos0, uint32_t n_heads,
-                              uint32_t n_kv_heads, uint32_t head_dim, hipStream_t st);
+                              uint32_t n_kv_heads, uint32_t head_dim, hipStream_t st,
+                              uint32_t in_stride = 0);
 
 // Decode: plan + launch. `fused` carries the prologue inputs for
 // flk_decode_layer (null q_raw means plain decode).

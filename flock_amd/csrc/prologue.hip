@@ -112,7 +112,7 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
     const float* __restrict__ v_raw, const float* __restrict__ gq, const float* __restrict__ gk,
     const float* __restrict__ inv_freq, float eps, int32_t pairing, float* __restrict__ qn_out,
     float* __restrict__ kcache, float* __restrict__ vcache, uint32_t pos0, uint32_t n_heads,
-    uint32_t n_kv_heads) {
+    uint32_t n_kv_heads, uint32_t q_stride, uint32_t kv_stride) {
   __shared__ float2 s_cs[D / 2];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
@@ -124,17 +124,17 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
   auto locate = [&](uint32_t idx, const float*& src, float*& dst, const float*& g) {
     g = nullptr;
     if (idx < n_heads) {
-      src = q_raw + ((size_t)tok * n_heads + idx) * D;
+      src = q_raw + (size_t)tok * q_stride + (size_t)idx * D;
       dst = qn_out + ((size_t)tok * n_heads + idx) * D;
       g = gq;
     } else if (idx < n_heads + n_kv_heads) {
       const uint32_t h = idx - n_heads;
-      src = k_raw + (size_t)tok * kv_row + (size_t)h * D;
+      src = k_raw + (size_t)tok * kv_stride + (size_t)h * D;
       dst = kcache + (size_t)pos * kv_row + (size_t)h * D;
       g = gk;
     } else {
       const uint32_t h = idx - n_heads - n_kv_heads;
-      src = v_raw + (size_t)tok * kv_row + (size_t)h * D;
+      src = v_raw + (size_t)tok * kv_stride + (size_t)h * D;
       dst = vcache + (size_t)pos * kv_row + (size_t)h * D;
     }
   };
@@ -206,15 +206,19 @@ hipError_t launch_qk_prologue(const float* q_raw, const float* k_raw, const floa
                               const float* gq, const float* gk, const float* inv_freq, float eps,
                               int32_t pairing, float* qn_out, float* kcache, float* vcache,
                               uint32_t n_tokens, uint32_t pos0, uint32_t n_heads,
-                              uint32_t n_kv_heads, uint32_t head_dim, hipStream_t st) {
+                              uint32_t n_kv_heads, uint32_t head_dim, hipStream_t st,
+                              uint32_t in_stride) {
+  // Raw rows of consecutive tokens: packed, or in_stride floats apart.
+  const uint32_t q_stride = in_stride ? in_stride : n_heads * head_dim;
+  const uint32_t kv_stride = in_stride ? in_stride : n_kv_heads * head_dim;
   if (head_dim == 128)
     hipLaunchKernelGGL(qk_prologue_kernel<128>, dim3(n_tokens), dim3(kPrologueThreads), 0, st,
                        q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
-                       vcache, pos0, n_heads, n_kv_heads);
+                       vcache, pos0, n_heads, n_kv_heads, q_stride, kv_stride);
   else
     hipLaunchKernelGGL(qk_prologue_kernel<64>, dim3(n_tokens), dim3(kPrologueThreads), 0, st,
                        q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
-                       vcache, pos0, n_heads, n_kv_heads);
+                       vcache, pos0, n_heads, n_kv_heads, q_stride, kv_stride);
   return hipGetLastError();
 }
 

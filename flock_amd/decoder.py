@@ -28,8 +28,10 @@ loads its input.)
 Every op keeps the reference's arithmetic, so the K/V rows this layer writes
 are bit-identical to layerForwardRef's and the output differs from it only
 through attention's summation order. Prefill runs the same ops over n tokens
-with the batched projection (token on grid y, layer_ref.ts:112-128) and the
-prologue + prefill attention kernels.
+(layer_ref.ts:112-128; 8 or more tokens take the weight-reusing tile
+projections): one projection over q|k|v into a [n][q|k|v] buffer, the
+prologue reading it strided (flk_qk_prologue_strided), prefill attention,
+then o, gate/up and down as in decode.
 """
 from __future__ import annotations
 
@@ -132,8 +134,7 @@ class DecoderLayer:
         B = ops.DeviceBuffer
         self.buf = {
             "h": B(P * hid * f), "h2": B(P * hid * f), "out": B(P * hid * f),
-            "qkv": B((H + 2 * Hkv) * d * f),
-            "q": B(P * H * d * f), "k": B(P * Hkv * d * f), "v": B(P * Hkv * d * f),
+            "qkv": B(P * (H + 2 * Hkv) * d * f),  # per token: q | k | v
             "qn": B(P * H * d * f), "attn": B(P * H * d * f),
             "gu": B(2 * ffn * f), "gate": B(P * ffn * f), "up": B(P * ffn * f),
             "act": B(P * ffn * f),
@@ -246,11 +247,14 @@ class DecoderLayer:
         self._hidden_in(nTokens, hidden)
         n = nTokens
         hin = b["h"] if src is None else src
-        for w, out in ((self.w_q, b["q"]), (self.w_k, b["k"]), (self.w_v, b["v"])):
-            ops.q8_matvec_ex(w, hin, out, n, norm_gain=g["attn_norm.weight"], eps=cfg.eps)
-        ops.qk_prologue(b["q"], b["k"], b["v"], g["attn_q_norm.weight"], g["attn_k_norm.weight"],
-                        b["invFreq"], cfg.eps, cfg.ropePairing, b["qn"], b["kcache"],
-                        b["vcache"], n, pos, H, Hkv, d, cfg.maxKeys)
+        # One projection over q|k|v stacked (layer.ts:722-724 runs three); the
+        # prologue reads each token's q, k and v rows out of its q|k|v row.
+        ops.q8_matvec_ex(self.w_qkv, hin, b["qkv"], n, norm_gain=g["attn_norm.weight"],
+                         eps=cfg.eps)
+        qkv, row = b["qkv"].ptr, (H + 2 * Hkv) * d
+        ops.qk_prologue(qkv, qkv + H * d * 4, qkv + (H + Hkv) * d * 4, g["attn_q_norm.weight"],
+                        g["attn_k_norm.weight"], b["invFreq"], cfg.eps, cfg.ropePairing, b["qn"],
+                        b["kcache"], b["vcache"], n, pos, H, Hkv, d, cfg.maxKeys, in_stride=row)
         ops.attn_prefill(b["qn"], b["kcache"], b["vcache"], b["attn"], H, Hkv, d, n, pos, self.ws)
         ops.q8_matvec_ex(self.w_o, b["attn"], b["h2"], n, res=hin)
         self._ffn(n, b["out"])

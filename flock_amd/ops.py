@@ -161,7 +161,16 @@ def kv_append(kn, v, kcache, vcache, n_tokens: int, pos0: int, n_kv_heads: int, 
 
 def qk_prologue(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps: float, pairing, qn_out, kcache,
                 vcache, n_tokens: int, pos0: int, n_heads: int, n_kv_heads: int, head_dim: int,
-                max_keys: int) -> None:
+                max_keys: int, in_stride: int = 0) -> None:
+    """flk_qk_prologue; in_stride > 0: raw rows of consecutive tokens lie that
+    many floats apart (flk_qk_prologue_strided, e.g. a q|k|v stacked output)."""
+    if in_stride:
+        check(lib().flk_qk_prologue_strided(ptr(q_raw), ptr(k_raw), ptr(v_raw), in_stride,
+                                            ptr(gq), ptr(gk), ptr(inv_freq), eps,
+                                            _pairing(pairing), ptr(qn_out), ptr(kcache),
+                                            ptr(vcache), n_tokens, pos0, n_heads, n_kv_heads,
+                                            head_dim, max_keys), "flk_qk_prologue_strided")
+        return
     check(lib().flk_qk_prologue(ptr(q_raw), ptr(k_raw), ptr(v_raw), ptr(gq), ptr(gk),
                                 ptr(inv_freq), eps, _pairing(pairing), ptr(qn_out), ptr(kcache),
                                 ptr(vcache), n_tokens, pos0, n_heads, n_kv_heads, head_dim,

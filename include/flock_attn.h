@@ -123,6 +123,20 @@ int32_t flk_qk_prologue(const float* q_raw, const float* k_raw, const float* v_r
                         uint32_t n_tokens, uint32_t pos0, uint32_t n_heads,
                         uint32_t n_kv_heads, uint32_t head_dim, uint32_t max_keys);
 
+/* Extension, no reference counterpart (layer.ts:722-724 projects q, k and v
+ * into three buffers): flk_qk_prologue reading raw rows that lie in_stride
+ * floats apart from one token to the next -- e.g. q_raw = qkv, k_raw = qkv +
+ * n_heads * head_dim, v_raw = k_raw + n_kv_heads * head_dim, in_stride = (n_heads
+ * + 2 * n_kv_heads) * head_dim for the output of ONE projection over q|k|v
+ * stacked row-wise. in_stride 0 means packed (flk_qk_prologue); otherwise it
+ * must be at least n_heads * head_dim. Same results. */
+int32_t flk_qk_prologue_strided(const float* q_raw, const float* k_raw, const float* v_raw,
+                                uint32_t in_stride, const float* gq, const float* gk,
+                                const float* inv_freq, float eps, int32_t pairing,
+                                float* qn_out, float* kcache, float* vcache, uint32_t n_tokens,
+                                uint32_t pos0, uint32_t n_heads, uint32_t n_kv_heads,
+                                uint32_t head_dim, uint32_t max_keys);
+
 /* -------------------------------------------------------------- attention -- */
 
 /* attention.wgsl main (attention.wgsl:58-122; bindings [q, kcache, vcache, o,

@@ -162,6 +162,16 @@ def test_q8_matvec_guards():
     assert rc == _lib.FLK_ERR_ARG and "norm_gain" in msg and "aligned" in msg
 
 
+def test_strided_prologue_guards():
+    L = _lib.lib()
+    args = (FAKE, FAKE, FAKE, 1e-6, 0, FAKE, FAKE, FAKE, 4, 0, 16, 8, 128, 64)
+    rc, msg = code_and_msg(L.flk_qk_prologue_strided(FAKE, FAKE, FAKE, 2047, *args))
+    assert rc == _lib.FLK_ERR_ARG and "in_stride" in msg
+    rc, msg = code_and_msg(L.flk_qk_prologue_strided(FAKE, FAKE, FAKE, 4096, FAKE, FAKE, FAKE, 1e-6,
+                                                     0, FAKE, FAKE, FAKE, 4, 62, 16, 8, 128, 64))
+    assert rc == _lib.FLK_ERR_CACHE_FULL
+
+
 def test_q8_split_matches_oracle():
     # Host-side repack (no GPU): the library's splitQ8 against the oracle's.
     import numpy as np

@@ -136,6 +136,19 @@ def test_prologue_bit_exact(rng, d, pairing, n, pos0):
     ops.kv_append(kb, dev(v), kc2, vc2, n, pos0, Hkv, d, maxk)
     assert np.array_equal(get(qb, n * H * d), got_q)
     assert np.array_equal(kc2.download(maxk * row)[pos0 * row:(pos0 + n) * row], got_k)
+    # The same rows read out of one [n][q | k | v] buffer (a stacked
+    # projection's output) by the strided entry point.
+    wide = (H + 2 * Hkv) * d
+    qkv = np.concatenate([q.reshape(n, H * d), k.reshape(n, Hkv * d), v.reshape(n, Hkv * d)],
+                         axis=1).ravel()
+    qkvb = dev(qkv)
+    kc3, vc3, qn3 = empty(maxk * Hkv * d), empty(maxk * Hkv * d), empty(n * H * d)
+    ops.qk_prologue(qkvb.ptr, qkvb.ptr + H * d * 4, qkvb.ptr + (H + Hkv) * d * 4, dev(gq), dev(gk),
+                    dev(inv), EPS, pairing, qn3, kc3, vc3, n, pos0, H, Hkv, d, maxk,
+                    in_stride=wide)
+    assert np.array_equal(get(qn3, n * H * d), got_q)
+    assert np.array_equal(kc3.download(maxk * row)[pos0 * row:(pos0 + n) * row], got_k)
+    assert np.array_equal(vc3.download(maxk * row)[pos0 * row:(pos0 + n) * row], got_v)
 
 
 # ------------------------------------------------------------------- decode --
