@@ -416,17 +416,22 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs
   }
 }
 
-// grid (head, column chunk, sequence); thread -> (group r, float4 column c).
-// Group r takes splits r, r + GROUPS, ...: each round issues up to
-// kMergeBatch independent loads per thread, folds them with weights against
-// the running max, and the groups combine through LDS in a fixed order (the
-// result does not depend on scheduling).
+// grid (head, column chunk, sequence); thread -> (group r, float4 column c),
+// lane = 8 * (r mod 8) + c. Group r takes splits r, r + GROUPS, ...: each
+// round issues up to kMergeBatch independent loads per thread and folds them
+// with weights against the running max. The groups then combine in a fixed
+// order (the result does not depend on scheduling): the workgroup's maximum
+// (lane butterfly, then the waves through LDS), one rescale per thread, and a
+// sum butterfly over the lanes of a column (strides 8, 16, 32) followed by
+// the waves in order.
 template <int D>
 __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs a) {
   constexpr int GROUPS = kMergeThreads / kMergeCols;
-  __shared__ float s_m[GROUPS];
-  __shared__ float s_l[GROUPS];
-  __shared__ float4 s_acc[GROUPS][kMergeCols];
+  constexpr int WAVES = kMergeThreads / kWave;
+  static_assert(kMergeCols == 8 && kWave == 64, "lane = 8 * (group mod 8) + column");
+  __shared__ float s_m[WAVES];
+  __shared__ float s_l[WAVES];
+  __shared__ float4 s_acc[WAVES][kMergeCols];
 
   const uint32_t head = blockIdx.x;
   const uint32_t seq = blockIdx.z;
@@ -475,28 +480,38 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs 
     }
     M = mx;
   }
-  if (tid % kMergeCols == 0) {
-    s_m[grp] = M;
-    s_l[grp] = L;
-  }
-  s_acc[grp][tid % kMergeCols] = A;
+  const int wave = tid / kWave, lane = tid % kWave;
+  float MM = fmaxf(M, xor_lane<8>(M));
+  MM = fmaxf(MM, xor_lane<16>(MM));
+  MM = fmaxf(MM, shfl_xor(MM, 32));
+  if (lane == 0) s_m[wave] = MM;
   __syncthreads();
-  if (grp != 0) return;
-  float MM = -INFINITY;
 #pragma unroll
-  for (int r = 0; r < GROUPS; r++) MM = fmaxf(MM, s_m[r]);
-  L = 0.f;
-  A = make_float4(0.f, 0.f, 0.f, 0.f);
+  for (int w = 0; w < WAVES; w++) MM = fmaxf(MM, s_m[w]);
+  const float wt = M == -INFINITY ? 0.f : expf(M - MM);
+  float v[5] = {L * wt, A.x * wt, A.y * wt, A.z * wt, A.w * wt};
 #pragma unroll
-  for (int r = 0; r < GROUPS; r++) {
-    const float mr = s_m[r];
-    const float w = mr == -INFINITY ? 0.f : expf(mr - MM);
-    L = fmaf(s_l[r], w, L);
-    const float4 p = s_acc[r][tid];
-    A.x = fmaf(p.x, w, A.x);
-    A.y = fmaf(p.y, w, A.y);
-    A.z = fmaf(p.z, w, A.z);
-    A.w = fmaf(p.w, w, A.w);
+  for (int k = 0; k < 5; k++) {
+    v[k] = v[k] + xor_lane<8>(v[k]);
+    v[k] = v[k] + xor_lane<16>(v[k]);
+    v[k] = v[k] + shfl_xor(v[k], 32);
+  }
+  if (lane < kMergeCols) {
+    if (lane == 0) s_l[wave] = v[0];
+    s_acc[wave][lane] = make_float4(v[1], v[2], v[3], v[4]);
+  }
+  __syncthreads();
+  if (tid >= kMergeCols) return;
+  L = s_l[0];
+  A = s_acc[0][tid];
+#pragma unroll
+  for (int w = 1; w < WAVES; w++) {
+    L += s_l[w];
+    const float4 p = s_acc[w][tid];
+    A.x += p.x;
+    A.y += p.y;
+    A.z += p.z;
+    A.w += p.w;
   }
   reinterpret_cast<float4*>(a.o + ((size_t)seq * a.n_heads + head) * D)[c] =
       make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
