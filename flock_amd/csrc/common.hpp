@@ -65,13 +65,47 @@ __device__ __forceinline__ float xor_lane(float v) {
   }
 }
 
+// gfx950 v_permlane16_swap / v_permlane32_swap with v in both operands: the
+// two results hold, in every lane i, v of lane i and of lane i ^ M (one of
+// each; which one is which depends on bit log2(M) of i). For a commutative op
+// op(lo, hi) is therefore the xor-M butterfly step in every lane, computed on
+// the VALU instead of through the LDS pipeline (ds_swizzle, ds_bpermute).
+// Needs every lane of the wave active.
+template <int M>
+__device__ __forceinline__ void swap_pair(float v, float& lo, float& hi) {
+  static_assert(M == 16 || M == 32, "swap_pair");
+  const int x = __builtin_bit_cast(int, v);
+  if constexpr (M == 16) {
+    const auto r = __builtin_amdgcn_permlane16_swap(x, x, false, false);
+    lo = __builtin_bit_cast(float, (int)r[0]);
+    hi = __builtin_bit_cast(float, (int)r[1]);
+  } else {
+    const auto r = __builtin_amdgcn_permlane32_swap(x, x, false, false);
+    lo = __builtin_bit_cast(float, (int)r[0]);
+    hi = __builtin_bit_cast(float, (int)r[1]);
+  }
+}
+// v + (v of lane i ^ M); the same float in both lanes (a + b == b + a).
+template <int M>
+__device__ __forceinline__ float sum_xor(float v) {
+  float lo, hi;
+  swap_pair<M>(v, lo, hi);
+  return lo + hi;
+}
+template <int M>
+__device__ __forceinline__ float max_xor(float v) {
+  float lo, hi;
+  swap_pair<M>(v, lo, hi);
+  return fmaxf(lo, hi);
+}
+
 // The pairwise tree over P lanes (P a power of two <= 64) as an xor
 // butterfly, strides P/2 .. 1: every lane of an aligned group of P ends with
 // the group's tree total.
 template <int P>
 __device__ __forceinline__ float lane_tree(float v) {
-  if constexpr (P >= 64) v = v + shfl_xor(v, 32);
-  if constexpr (P >= 32) v = v + xor_lane<16>(v);
+  if constexpr (P >= 64) v = sum_xor<32>(v);
+  if constexpr (P >= 32) v = sum_xor<16>(v);
   if constexpr (P >= 16) v = v + xor_lane<8>(v);
   // After the stride-8 step lanes j and j ^ 8 hold the same float, so one
   // row_ror:4 (lane i - 4, i.e. i ^ 4 or (i ^ 4) ^ 8) serves as xor 4.
@@ -93,9 +127,8 @@ __device__ __forceinline__ float group_sum(float v) {
   if (width >= 4) v += dpp<kDppXor2>(v);
   if (width >= 8) v += dpp<kDppHalfMirror>(v);
   if (width >= 16) v += dpp<kDppMirror>(v);
-  if (width >= 32)  // swap the two 16-lane halves of each 32-lane group
-    v += __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
-  if (width >= 64) v += shfl_xor(v, 32);
+  if (width >= 32) v = sum_xor<16>(v);  // the two 16-lane halves of each 32-lane group
+  if (width >= 64) v = sum_xor<32>(v);
   return v;
 }
 
@@ -109,13 +142,14 @@ __device__ __forceinline__ float group_sum(float v) {
 // in lane i equals tree[i mod stride], and addition is commutative).
 //
 // tree_sum64 is that butterfly (strides 32, 16, ..., 1, every lane adding its
-// partner i ^ stride) with the in-row strides on DPP: 8 is row_ror:8 (exactly
+// partner i ^ stride) with 32 and 16 on the permlane swaps and the in-row
+// strides on DPP: 8 is row_ror:8 (exactly
 // i ^ 8); 4 is row_ror:4, which reads lane (i - 4) mod 16 -- that is i ^ 4
 // or (i ^ 4) ^ 8, and after the stride-8 step lanes j and j ^ 8 hold the same
 // float (a + b and b + a), so it is the same value; 2 and 1 are quad_perm.
 __device__ __forceinline__ float tree_sum64(float p) {
-  p = p + shfl_xor(p, 32);
-  p = p + __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, p), 0x401F));
+  p = sum_xor<32>(p);
+  p = sum_xor<16>(p);
   p = p + dpp<kDppRor8>(p);
   p = p + dpp<kDppRor4>(p);
   p = p + dpp<kDppXor2>(p);

@@ -482,8 +482,8 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs 
   }
   const int wave = tid / kWave, lane = tid % kWave;
   float MM = fmaxf(M, xor_lane<8>(M));
-  MM = fmaxf(MM, xor_lane<16>(MM));
-  MM = fmaxf(MM, shfl_xor(MM, 32));
+  MM = max_xor<16>(MM);
+  MM = max_xor<32>(MM);
   if (lane == 0) s_m[wave] = MM;
   __syncthreads();
 #pragma unroll
@@ -493,8 +493,8 @@ __global__ __launch_bounds__(kMergeThreads) void decode_merge_kernel(DecodeArgs 
 #pragma unroll
   for (int k = 0; k < 5; k++) {
     v[k] = v[k] + xor_lane<8>(v[k]);
-    v[k] = v[k] + xor_lane<16>(v[k]);
-    v[k] = v[k] + shfl_xor(v[k], 32);
+    v[k] = sum_xor<16>(v[k]);
+    v[k] = sum_xor<32>(v[k]);
   }
   if (lane < kMergeCols) {
     if (lane == 0) s_l[wave] = v[0];

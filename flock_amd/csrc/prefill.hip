@@ -15,7 +15,8 @@
 //                   S^T[key 4(l/16)+i][row l%16].
 //   softmax         every column (one query-head row) lives in lanes with the
 //                   same l%16: in-lane max/sum over 16 values, then lane xor
-//                   16 and 32. Running (m, l) per lane, no LDS.
+//                   16 and 32 (permlane swaps). Running (m, l) per lane, no
+//                   LDS.
 //   O^T += V^T P^T  B = P^T taken directly from the S^T registers (the key
 //                   order inside a k-step is permuted identically on both
 //                   operands); A = V^T read from LDS. Output row m of channel
@@ -259,8 +260,8 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
           mx = fmaxf(mx, t);
         }
     }
-    mx = fmaxf(mx, shfl_xor(mx, 16));
-    mx = fmaxf(mx, shfl_xor(mx, 32));
+    mx = max_xor<16>(mx);
+    mx = max_xor<32>(mx);
     const float mn = fmaxf(m_run, mx);
     float corr = 1.f, rs = 0.f;
     if (mn != -INFINITY) {
@@ -277,8 +278,8 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
 #pragma unroll
       for (int b = 0; b < kHalfKB; b++) sacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
     }
-    rs += shfl_xor(rs, 16);
-    rs += shfl_xor(rs, 32);
+    rs = sum_xor<16>(rs);
+    rs = sum_xor<32>(rs);
     l_run = l_run * corr + rs;
     m_run = mn;
 #pragma unroll
