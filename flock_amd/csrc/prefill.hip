@@ -145,11 +145,14 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   const int lc = lane & 15;    // column within the 16-block = row of this lane
   const int lg = lane >> 4;    // lane group 0..3
   // V-read swizzle (D = 128): A-operand lane lc supplies channel 8*lc + (c ^
-  // 4*sw_rd) of block c, so output row m of the O^T accumulators holds channel
-  // 8*m + (c ^ 4*((m >> 3) & 1)); for this lane's rows m = 4*lg + j that bit
-  // is sw_wr.
-  const int sw_rd = CB == 8 ? (lc >> 3) & 1 : 0;
-  const int sw_wr = CB == 8 ? (lg >> 1) & 1 : 0;
+  // 4*sw(lc)) of block c with sw(m) = ((m >> 2) ^ (m >> 3)) & 1, so the two
+  // float4s of a key row are read in swapped order by lanes lc and lc ^ 4 and
+  // by lanes lc and lc ^ 8: any 8 consecutive lanes cover 32 distinct banks
+  // and any 16 cover 64. Output row m of the O^T accumulators then holds
+  // channel 8*m + (c ^ 4*sw(m)); for this lane's rows m = 4*lg + j that is
+  // sw_wr.
+  const int sw_rd = CB == 8 ? ((lc >> 2) ^ (lc >> 3)) & 1 : 0;
+  const int sw_wr = CB == 8 ? (lg ^ (lg >> 1)) & 1 : 0;
   const uint32_t n_keys_total = a.pos0 + a.n_queries;
   const uint32_t q0 = qt * a.q_per_tile;
 
@@ -196,44 +199,76 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   load_tile<D>(pk, pv, a, kvh, kt0 + 1 < kt1 ? kt0 + 1 : kt0, n_keys_total, tid);
   __syncthreads();
 
+  // Operands are read from LDS kAhead groups ahead of the MFMAs that use
+  // them; sched_barrier keeps the compiler from sinking each read next to its
+  // first use, where every group's LDS latency would stall the wave.
+  constexpr int kAhead = 2;
+  constexpr int NG = DS / 4;        // S: groups of 4 k-steps (one float4 per chain)
+  constexpr int NST = kHalfKB * 4;  // PV: k-steps of 4 keys
+  const float* kr0 = &k_lds[((half * kHalfKB) * 16 + lc) * LDK + DS * lg];
+  const float* vr0 = &v_lds[((half * kHalfKB) * 16 + 4 * lg) * D + CB * lc];
+  auto k_group = [&](const float* kt_lds_base, int g, int b) {
+    return *reinterpret_cast<const floatx4*>(kt_lds_base + b * 16 * LDK + 4 * g);
+  };
+  auto v_step = [&](const float* vt_lds_base, int st, int c4) {
+    const int b = st / 4, i = st % 4;
+    // Lanes 8..15 of a row group read their float4s in the other order, so
+    // the 16 lanes hit 16 distinct 16-byte bank slots.
+    return *reinterpret_cast<const floatx4*>(vt_lds_base + (b * 16 + i) * D + 4 * (c4 ^ sw_rd));
+  };
+
   for (uint32_t kt = kt0; kt < kt1; kt++) {
     const uint32_t key0 = kt * kBK;
     const int buf = (kt - kt0) & 1;
-    const float* kt_lds = k_lds + buf * (kBK * LDK);
-    const float* vt_lds = v_lds + buf * (kBK * D);
-    if (kt + 1 < kt1) {
-      store_tile<D>(pk, pv, k_lds + (buf ^ 1) * (kBK * LDK), v_lds + (buf ^ 1) * (kBK * D),
-                    kt + 1, n_keys_total, tid);
-      // The tile after (the last one is simply loaded again at the end).
-      load_tile<D>(pk, pv, a, kvh, kt + 2 < kt1 ? kt + 2 : kt + 1, n_keys_total, tid);
-    }
+    const float* kb = kr0 + buf * (kBK * LDK);
+    const float* vb = vr0 + buf * (kBK * D);
+
+    // The first K groups of this tile (stored before the last barrier).
+    floatx4 kg[kAhead + 1][kHalfKB];
+#pragma unroll
+    for (int g = 0; g < kAhead; g++)
+#pragma unroll
+      for (int b = 0; b < kHalfKB; b++) kg[g][b] = k_group(kb, g, b);
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- S^T = K Q^T ------------------------------------------------------------
     // Each MFMA depends on the previous one of its block's chain, so the
     // blocks' chains are issued interleaved, step by step.
     floatx4 sacc[kHalfKB];
-    {
-      float kf[kHalfKB][DS];
 #pragma unroll
-      for (int b = 0; b < kHalfKB; b++) {
-        const float* kr = &kt_lds[((half * kHalfKB + b) * 16 + lc) * LDK + DS * lg];
+    for (int b = 0; b < kHalfKB; b++) sacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
 #pragma unroll
-        for (int s4 = 0; s4 < DS / 4; s4++) {
-          const float4 v = *reinterpret_cast<const float4*>(kr + 4 * s4);
-          kf[b][4 * s4 + 0] = v.x;
-          kf[b][4 * s4 + 1] = v.y;
-          kf[b][4 * s4 + 2] = v.z;
-          kf[b][4 * s4 + 3] = v.w;
-        }
+    for (int g = 0; g < NG; g++) {
+      if (g + kAhead < NG) {
+#pragma unroll
+        for (int b = 0; b < kHalfKB; b++) kg[(g + kAhead) % (kAhead + 1)][b] = k_group(kb, g + kAhead, b);
       }
+      __builtin_amdgcn_sched_barrier(0);
+      // Halfway through S (the MFMAs queued so far cover the writes), tile
+      // kt + 1 goes from registers into the other buffer and tile kt + 2 is
+      // requested (the last one is simply loaded again at the end).
+      if (g == NG / 2 && kt + 1 < kt1) {
+        store_tile<D>(pk, pv, k_lds + (buf ^ 1) * (kBK * LDK), v_lds + (buf ^ 1) * (kBK * D),
+                      kt + 1, n_keys_total, tid);
+        load_tile<D>(pk, pv, a, kvh, kt + 2 < kt1 ? kt + 2 : kt + 1, n_keys_total, tid);
+      }
+      __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
-      for (int b = 0; b < kHalfKB; b++) sacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-      for (int s = 0; s < DS; s++)
+      for (int j = 0; j < 4; j++)
 #pragma unroll
         for (int b = 0; b < kHalfKB; b++)
-          sacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kf[b][s], qreg[s], sacc[b], 0, 0, 0);
+          sacc[b] = __builtin_amdgcn_mfma_f32_16x16x4f32(kg[g % (kAhead + 1)][b][j], qreg[4 * g + j],
+                                                         sacc[b], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
     }
+
+    // The first V steps go out before the softmax, which does not need them.
+    floatx4 vg[kAhead + 1][CB / 4];
+#pragma unroll
+    for (int st = 0; st < kAhead; st++)
+#pragma unroll
+      for (int c4 = 0; c4 < CB / 4; c4++) vg[st][c4] = v_step(vb, st, c4);
+    __builtin_amdgcn_sched_barrier(0);
 
     // ---- online softmax of this lane's row (base 2) ----------------------------
     // Scores are kept as log2-scaled values t = (q.k) * scale * log2(e), so
@@ -287,25 +322,19 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
 
     // ---- O^T += V^T P^T ---------------------------------------------------------
 #pragma unroll
-    for (int b = 0; b < kHalfKB; b++)
+    for (int st = 0; st < NST; st++) {
+      if (st + kAhead < NST) {
 #pragma unroll
-      for (int i = 0; i < 4; i++) {
-        const float* vr = &vt_lds[((half * kHalfKB + b) * 16 + 4 * lg + i) * D + CB * lc];
-        float vv[CB];
-#pragma unroll
-        for (int c4 = 0; c4 < CB / 4; c4++) {
-          // Lanes 8..15 of a row group read their two float4s in the other
-          // order, so the 16 lanes hit 16 distinct 16-byte bank slots.
-          const float4 v = *reinterpret_cast<const float4*>(vr + 4 * (c4 ^ sw_rd));
-          vv[4 * c4 + 0] = v.x;
-          vv[4 * c4 + 1] = v.y;
-          vv[4 * c4 + 2] = v.z;
-          vv[4 * c4 + 3] = v.w;
-        }
-#pragma unroll
-        for (int c = 0; c < CB; c++)
-          oacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vv[c], sacc[b][i], oacc[c], 0, 0, 0);
+        for (int c4 = 0; c4 < CB / 4; c4++)
+          vg[(st + kAhead) % (kAhead + 1)][c4] = v_step(vb, st + kAhead, c4);
       }
+      __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
+      for (int c = 0; c < CB; c++)
+        oacc[c] = __builtin_amdgcn_mfma_f32_16x16x4f32(vg[st % (kAhead + 1)][c / 4][c % 4],
+                                                       sacc[st / 4][st % 4], oacc[c], 0, 0, 0);
+      __builtin_amdgcn_sched_barrier(0);
+    }
     __syncthreads();  // tile kt + 1 stored; buffer of tile kt free again
   }
 
