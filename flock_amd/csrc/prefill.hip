@@ -51,6 +51,9 @@ constexpr int kHalfKB = 2;      // 16-key blocks per wave per tile
 constexpr uint32_t kMinPairedWG = 192;    // paired mode when it yields this many
 constexpr uint32_t kTargetSplitWG = 256;  // split mode aims at one workgroup per CU
 constexpr uint32_t kMinKtPerSplit = 2;
+#ifndef FLK_PREFILL_AHEAD
+#define FLK_PREFILL_AHEAD 1  // operand groups read from LDS ahead of their MFMAs
+#endif
 
 struct PrefillArgs {
   const float* q;
@@ -202,7 +205,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   // Operands are read from LDS kAhead groups ahead of the MFMAs that use
   // them; sched_barrier keeps the compiler from sinking each read next to its
   // first use, where every group's LDS latency would stall the wave.
-  constexpr int kAhead = 2;
+  constexpr int kAhead = FLK_PREFILL_AHEAD;
   constexpr int NG = DS / 4;        // S: groups of 4 k-steps (one float4 per chain)
   constexpr int NST = kHalfKB * 4;  // PV: k-steps of 4 keys
   const float* kr0 = &k_lds[((half * kHalfKB) * 16 + lc) * LDK + DS * lg];
@@ -212,8 +215,6 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   };
   auto v_step = [&](const float* vt_lds_base, int st, int c4) {
     const int b = st / 4, i = st % 4;
-    // Lanes 8..15 of a row group read their float4s in the other order, so
-    // the 16 lanes hit 16 distinct 16-byte bank slots.
     return *reinterpret_cast<const floatx4*>(vt_lds_base + (b * 16 + i) * D + 4 * (c4 ^ sw_rd));
   };
 
