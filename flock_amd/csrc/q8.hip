@@ -540,7 +540,17 @@ template <int S, int N, int I = 0>
 __device__ __forceinline__ void q8_halve_step(float (&v)[32], bool hi) {
   if constexpr (I < N / 2) {
     const float lo = v[I], up = v[I + N / 2];
-    v[I] = (hi ? up : lo) + xor_lane<S>(hi ? lo : up);
+    if constexpr (S == 16) {
+      // v_permlane16_swap(lo, up) trades the odd rows of lo for the even rows
+      // of up: a lane with bit 4 clear then holds its own lo and its
+      // partner's lo, a lane with it set its partner's up and its own up --
+      // exactly the pair the step adds, with no selects.
+      const auto r = __builtin_amdgcn_permlane16_swap(__builtin_bit_cast(int, lo),
+                                                      __builtin_bit_cast(int, up), false, false);
+      v[I] = __builtin_bit_cast(float, (int)r[0]) + __builtin_bit_cast(float, (int)r[1]);
+    } else {
+      v[I] = (hi ? up : lo) + xor_lane<S>(hi ? lo : up);
+    }
     q8_halve_step<S, N, I + 1>(v, hi);
   }
 }
