@@ -190,6 +190,22 @@ def test_decode_north_star_bar(rng, d, nk):
     assert np.array_equal(argmax_rows(got, H), argmax_rows(want, H)), top2_margin(want, H)
 
 
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("H,Hkv,nk", [(12, 4, 700), (24, 4, 1500), (16, 2, 2049), (8, 1, 513),
+                                      (32, 4, 300), (6, 2, 4097)])
+def test_decode_group_sizes(rng, d, H, Hkv, nk):
+    # GQA groups 3, 6, 8 and 8 with one kv head per workgroup (KH = 1, 2, 4):
+    # the template cases Qwen3's 16 / 8 layout never reaches, with key splits.
+    q = randn(rng, H * d)
+    k, v = randn(rng, nk * Hkv * d), randn(rng, nk * Hkv * d)
+    got = _decode(q, k, v, H, Hkv, d, nk)
+    want = oracle.attn(q, k, v, H, Hkv, d, nk)
+    m = metrics(got, want, cf.attention(q, k, v, H, Hkv, d, 1, nk - 1))
+    print(fmt(m))
+    assert meets_bar(m), fmt(m)
+    assert np.array_equal(argmax_rows(got, H), argmax_rows(want, H)), top2_margin(want, H)
+
+
 def test_decode_gqa_planted_kat():
     # test_ops.ts:357-392: heads 0,1 read kv head 0 (all 7), heads 2,3 read kv
     # head 1 (all -3), exactly.
