@@ -44,24 +44,23 @@ constexpr int kDppRor12 = 0x12C;      // row_ror:12, lane i <- (i + 4) mod 16 wi
 constexpr int kDppHalfMirror = 0x141; // lane i <- 7 - i within 8
 constexpr int kDppMirror = 0x140;     // lane i <- 15 - i within 16
 
-// v of lane i ^ M, for M = 1, 2, 4, 8, 16 without LDS traffic: quad_perm for
+// v of lane i ^ M, for M = 1, 2, 4, 8, on DPP (no LDS traffic): quad_perm for
 // 1 and 2, row_ror:8 (exactly i ^ 8) for 8, row_ror:12 or :4 for 4 (lane i
-// with bit 2 clear reads i + 4, with it set i - 4), ds_swizzle for 16.
-// (row_ror:n hands lane i the value of lane (i - n) mod 16 of its row.)
+// with bit 2 clear reads i + 4, with it set i - 4). (row_ror:n hands lane i
+// the value of lane (i - n) mod 16 of its row.) Strides 16 and 32 leave the
+// row: see swap_pair.
 template <int M>
 __device__ __forceinline__ float xor_lane(float v) {
-  static_assert(M == 1 || M == 2 || M == 4 || M == 8 || M == 16, "xor_lane");
+  static_assert(M == 1 || M == 2 || M == 4 || M == 8, "xor_lane");
   if constexpr (M == 1) {
     return dpp<kDppXor1>(v);
   } else if constexpr (M == 2) {
     return dpp<kDppXor2>(v);
   } else if constexpr (M == 8) {
     return dpp<kDppRor8>(v);
-  } else if constexpr (M == 4) {
+  } else {
     const float up = dpp<kDppRor12>(v), down = dpp<kDppRor4>(v);  // lanes i + 4, i - 4
     return (threadIdx.x & 4) ? down : up;
-  } else {
-    return __builtin_bit_cast(float, __builtin_amdgcn_ds_swizzle(__builtin_bit_cast(int, v), 0x401F));
   }
 }
 
