@@ -51,7 +51,10 @@ constexpr int kQ8Threads = 256;   // 4 waves
 template <int NB>
 constexpr int q8_unroll() { return NB == 1 ? FLK_Q8_UNROLL : (NB == 2 ? 2 : 1); }
 constexpr int kQ8MaxRegBlocks = 4;  // x blocks per lane kept in registers (8192 columns)
-constexpr uint32_t kQ8LdsTreeRows = 65536;  // rows from which the lane tree uses the LDS unit
+#ifndef FLK_Q8_LDS_TREE_ROWS
+#define FLK_Q8_LDS_TREE_ROWS 65536
+#endif
+constexpr uint32_t kQ8LdsTreeRows = FLK_Q8_LDS_TREE_ROWS;  // rows from which the lane tree uses the LDS unit
 
 struct Q8Args {
   const uint8_t* qs;
