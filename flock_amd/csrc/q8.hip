@@ -387,7 +387,10 @@ constexpr int kMmTokenStride = 32 * kMmPad;  // floats per staged token
 // Row tiles one workgroup streams through its staged tokens (rows of one
 // chunk), at most; fewer when the grid would otherwise leave CUs idle.
 constexpr uint32_t kMmRowTiles = FLK_Q8_MM_ROW_TILES;
-constexpr uint32_t kMmMinWorkgroups = 1024;  // 4 per CU
+#ifndef FLK_Q8_MM_MIN_WG
+#define FLK_Q8_MM_MIN_WG 1024  // 4 per CU
+#endif
+constexpr uint32_t kMmMinWorkgroups = FLK_Q8_MM_MIN_WG;
 
 // One block of RT rows (weights w0/w1, scales sc) against the staged tokens,
 // folded into acc[r][t] (q8_coop.wgsl:105-112 per output). Per word pair g,
