@@ -102,9 +102,17 @@ int32_t flk_alloc(void** dptr, uint64_t bytes) {
 
 int32_t flk_free(void* dptr) {
   if (dptr == nullptr) return FLK_OK;
-  // Work still queued may read this buffer (a caller can drop its last
-  // reference right after a launch), so drain the device first.
-  hipError_t e = hipDeviceSynchronize();
+  // A free cannot be recorded into a graph, and hipFree would end a capture
+  // in progress: refuse it while the library stream is capturing.
+  if (g_stream != nullptr) {
+    hipStreamCaptureStatus cs = hipStreamCaptureStatusNone;
+    if (hipStreamIsCapturing(g_stream, &cs) == hipSuccess && cs != hipStreamCaptureStatusNone)
+      return fail(FLK_ERR_ARG, "flk_free while the library stream is capturing a graph");
+  }
+  // Work queued on the library stream may still read this buffer (a caller
+  // can drop its last reference right after a launch): wait for that stream.
+  // hipFree then waits for the rest of the device by itself.
+  hipError_t e = hipStreamSynchronize(g_stream);
   if (e == hipSuccess) e = hipFree(dptr);
   return hip_status(e, "hipFree");
 }
@@ -328,6 +336,9 @@ static int32_t decode_layer_common(const float* q_raw, const float* k_raw, const
   FLK_NONNULL(kcache);
   FLK_NONNULL(vcache);
   FLK_NONNULL(o);
+  FLK_ALIGNED(q_raw);  // the raw q, k, v rows are read as float4s too
+  FLK_ALIGNED(k_raw);
+  FLK_ALIGNED(v_raw);
   FLK_ALIGNED(qn_out);
   FLK_ALIGNED(kcache);
   FLK_ALIGNED(vcache);

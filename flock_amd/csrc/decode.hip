@@ -103,9 +103,16 @@ __device__ __forceinline__ uint32_t seq_splits(const DecodeArgs& a, uint32_t n_k
 
 // Keys sequence `seq` attends: the argument for one sequence; for a ragged
 // batch its n_keys entry, clamped to the planned bound so that the grid covers
-// every split (n_keys == 0 marks an empty sequence).
+// every split (n_keys == 0 marks an empty sequence). The fused layer call with
+// the key count in device memory (flk_decode_layer_dev) accepts only 1 ..
+// max_keys there: any other value gives 0, and the split kernel then fills o
+// with NaN and appends nothing (the reference throws "KV cache full" on the
+// host, layer.ts:575; a replayed graph has no host step to throw from).
 __device__ __forceinline__ uint32_t seq_keys(const DecodeArgs& a, uint32_t seq) {
-  return a.n_keys_dev != nullptr ? min(a.n_keys_dev[seq], a.n_keys) : a.n_keys;
+  if (a.n_keys_dev == nullptr) return a.n_keys;
+  const uint32_t v = a.n_keys_dev[seq];
+  if (a.q_raw != nullptr) return v <= a.n_keys ? v : 0u;
+  return min(v, a.n_keys);
 }
 
 // U keys of one slot: rows base + u * PH + ph. Past the end of the split the
@@ -198,7 +205,7 @@ __device__ __forceinline__ void attend_keys(const float4 (&kr_in)[U], const floa
 template <int D, int G, int KH>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs a) {
   constexpr int LPK = D / 4;                    // lanes per (key, kv head) row
-  constexpr int SLOTS = kDecodeThreads / LPK;   // 8 (D = 128) or 16 (D = 64)
+  constexpr int SLOTS = kDecodeThreads / LPK;   // 16 (D = 128) or 32 (D = 64) at 512 threads
   static_assert(SLOTS % KH == 0, "KH must divide the slot count");
   constexpr int PH = SLOTS / KH;                // key phases
   constexpr int U = decode_unroll(G);
@@ -228,10 +235,12 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs
 
   const uint32_t n_keys = seq_keys(a, seq);
   const uint64_t row0 = a.seq_row_off != nullptr ? a.seq_row_off[seq] : 0;
-  if (n_keys == 0) {  // empty ragged sequence: zero output rows
-    if (split == 0)
+  if (n_keys == 0) {  // empty ragged sequence: zero rows; bad device position: NaN rows
+    if (split == 0) {
+      const float fill = a.q_raw != nullptr ? __builtin_nanf("") : 0.f;
       for (int i = tid; i < HG * D; i += kDecodeThreads)
-        a.o[((size_t)seq * a.n_heads + h0) * D + i] = 0.f;
+        a.o[((size_t)seq * a.n_heads + h0) * D + i] = fill;
+    }
     return;
   }
   const uint32_t n_splits = seq_splits(a, n_keys);

@@ -25,8 +25,24 @@ def _pairing(p) -> int:
     return int(p)
 
 
+# Device pointers of buffers that were garbage-collected. flk_free waits for
+# the device, so a collection must not free on the spot (it could stall a
+# timed loop, or land inside a graph capture); the pointers are released at
+# the next sync() or release_pending().
+_pending_free: list[int] = []
+
+
+def release_pending() -> None:
+    """Free the buffers collected since the last sync() (waits for the device)."""
+    while _pending_free:
+        check(lib().flk_free(_pending_free.pop()), "flk_free")
+
+
 class DeviceBuffer:
-    """Device memory from flk_alloc (the reference's storageBuffer)."""
+    """Device memory from flk_alloc (the reference's storageBuffer).
+
+    free() releases it at once (flk_free waits for the device); a buffer that
+    is simply dropped is released at the next sync() / release_pending()."""
 
     def __init__(self, nbytes: int):
         if nbytes <= 0:
@@ -61,14 +77,14 @@ class DeviceBuffer:
 
     def free(self) -> None:
         if getattr(self, "ptr", None):
-            lib().flk_free(self.ptr)
+            check(lib().flk_free(self.ptr), "flk_free")
             self.ptr = None
 
     def __del__(self):
-        try:
-            self.free()
-        except Exception:
-            pass
+        p = getattr(self, "ptr", None)
+        if p:
+            _pending_free.append(p)
+            self.ptr = None
 
 
 def ptr(x) -> int | None:
@@ -119,7 +135,9 @@ def set_stream(stream) -> None:
 
 
 def sync() -> None:
+    """Wait for the library stream, then release dropped buffers."""
     check(lib().flk_sync(), "flk_sync")
+    release_pending()
 
 
 def device_count() -> int:

@@ -32,6 +32,9 @@
  *     whose plan has a single split needs none (ws may then be NULL).
  *   - head_dim must be 64 or 128; n_heads must be a multiple of n_kv_heads
  *     with n_heads / n_kv_heads <= 8.
+ *   - The attention kernels move 16-byte vectors: q, qn, o, kcache, vcache and
+ *     (flk_decode_layer) q_raw, k_raw, v_raw must be 16-byte aligned; a
+ *     misaligned pointer is rejected with FLK_ERR_ARG before any launch.
  */
 #ifndef FLOCK_ATTN_H
 #define FLOCK_ATTN_H
@@ -67,8 +70,11 @@ int32_t flk_device_count(int32_t* count);
 int32_t flk_set_stream(void* stream);
 
 /* Device memory (storageBuffer / createBuffer, lib.ts:548-566; readBack,
- * lib.ts:575-593). flk_h2d/flk_d2h are synchronous with respect to the host;
- * flk_free waits for all queued device work before releasing the memory. */
+ * lib.ts:575-593). flk_h2d/flk_d2h are synchronous with respect to the host.
+ * flk_free waits for the library stream, then releases the memory with
+ * hipFree, which waits for the rest of the device: call it outside loops that
+ * must not stall. While the library stream is capturing a graph it returns
+ * FLK_ERR_ARG and frees nothing (free after flk_capture_end). */
 int32_t flk_alloc(void** dptr, uint64_t bytes);
 int32_t flk_free(void* dptr);
 int32_t flk_h2d(void* dst, const void* host_src, uint64_t bytes, uint64_t dst_off);
@@ -143,7 +149,9 @@ int32_t flk_qk_prologue_strided(const float* q_raw, const float* k_raw, const fl
  * Dims{n_heads, n_kv_heads, head_dim, n_keys}], dispatch layer.ts:624-630).
  * One query per head attends keys [0, n_keys). No cap on n_keys beyond the
  * cache (the reference's $MAX_KEYS workgroup array, lib.ts:503-508, is gone):
- * split-K flash-decoding with an in-kernel log-sum-exp merge. */
+ * split-K flash-decoding -- a split kernel, then a log-sum-exp merge launch
+ * ordered after it on the same stream (one launch when the plan has a single
+ * split). */
 int32_t flk_attn_decode(const float* q, const float* kcache, const float* vcache, float* o,
                         uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                         uint32_t n_keys, void* ws, uint64_t ws_bytes);

@@ -21,10 +21,13 @@ extern "C" {
 #endif
 
 /* flk_decode_layer with the key count in device memory: *n_keys_dev = pos + 1,
- * at most max_keys (larger values are clamped to max_keys; the caller keeps
- * pos < max_keys, as the host guard of flk_decode_layer would). The launch
- * shape depends only on max_keys, so the call can be captured once and
- * replayed at every position. ws: flk_workspace_bytes(..., max_keys, 0, 1). */
+ * 1 <= *n_keys_dev <= max_keys. The launch shape depends only on max_keys, so
+ * the call can be captured once and replayed at every position. ws:
+ * flk_workspace_bytes(..., max_keys, 0, 1). The host cannot see the value, so
+ * the kernel checks it: 0 or a value above max_keys (a cache that is full,
+ * where flk_decode_layer returns FLK_ERR_CACHE_FULL) appends nothing, leaves
+ * qn_out as it was and fills o with NaN, which the LM head's argmax never
+ * selects (an all-NaN row yields its sentinel index 0xffffffff). */
 int32_t flk_decode_layer_dev(const float* q_raw, const float* k_raw, const float* v_raw,
                              const float* gq, const float* gk, const float* inv_freq, float eps,
                              int32_t pairing, float* qn_out, float* kcache, float* vcache,

@@ -185,3 +185,31 @@ def test_q8_split_matches_oracle():
                                    sc.ctypes.data) == 0
     want_qs, want_sc = oracle.split_q8(packed, rows, cols)
     assert np.array_equal(qs, want_qs) and np.array_equal(sc, want_sc)
+
+
+@pytest.mark.parametrize("which", ["q_raw", "k_raw", "v_raw"])
+def test_decode_layer_rejects_misaligned_raw_rows(which):
+    # The fused layer call reads the raw q, k, v rows as float4s: a pointer
+    # off a 16-byte boundary is refused on the host, for both position forms.
+    L = _lib.lib()
+    raw = {"q_raw": FAKE, "k_raw": FAKE, "v_raw": FAKE}
+    raw[which] = FAKE + 4
+    rest = (FAKE, FAKE, FAKE, 1e-6, 0, FAKE, FAKE, FAKE, FAKE)
+    rc, msg = code_and_msg(L.flk_decode_layer(raw["q_raw"], raw["k_raw"], raw["v_raw"], *rest,
+                                              10, 16, 8, 128, 2048, FAKE, 1 << 30))
+    assert rc == _lib.FLK_ERR_ARG and which in msg and "aligned" in msg
+    rc, msg = code_and_msg(L.flk_decode_layer_dev(raw["q_raw"], raw["k_raw"], raw["v_raw"], *rest,
+                                                  FAKE, 16, 8, 128, 2048, FAKE, 1 << 30))
+    assert rc == _lib.FLK_ERR_ARG and which in msg and "aligned" in msg
+
+
+def test_dropped_buffers_are_freed_at_sync_not_on_collection():
+    # A DeviceBuffer that is garbage-collected must not call flk_free (which
+    # waits for the device) on the spot; its pointer is parked until sync().
+    from flock_amd import ops
+    b = ops.DeviceBuffer.__new__(ops.DeviceBuffer)  # no allocation: a stand-in pointer
+    b.ptr, b.nbytes = FAKE, 4
+    before = list(ops._pending_free)
+    del b
+    assert ops._pending_free == before + [FAKE]
+    ops._pending_free.remove(FAKE)

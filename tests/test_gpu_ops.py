@@ -230,10 +230,15 @@ def test_decode_deterministic_across_runs(rng):
     assert all(np.array_equal(x, outs[0]) for x in outs)
 
 
-def test_decode_layer_fused_matches_oracle(rng):
+@pytest.mark.parametrize("H,Hkv", [(16, 8), (12, 4), (8, 1)])
+@pytest.mark.parametrize("d", [64, 128])
+@pytest.mark.parametrize("pairing", ["neox", "norm"])
+def test_decode_layer_fused_matches_oracle(rng, H, Hkv, d, pairing):
     # Layer.encode's attention slice in one launch (layer.ts:571-630) vs the
-    # oracle's layerForwardRef slice (layer_ref.ts:46-70).
-    H, Hkv, d, pos = 16, 8, 128, 700
+    # oracle's layerForwardRef slice (layer_ref.ts:46-70). The in-kernel
+    # prologue has a d = 64 branch (partner lane xor 32), the norm pairing,
+    # and workgroups holding 8, 4 or 1 kv heads with GQA groups of 2, 3, 8.
+    pos = 700
     maxk = 1024
     kc0, vc0 = randn(rng, maxk * Hkv * d), randn(rng, maxk * Hkv * d)
     q, k, v = randn(rng, H * d), randn(rng, Hkv * d), randn(rng, Hkv * d)
@@ -243,14 +248,52 @@ def test_decode_layer_fused_matches_oracle(rng):
     kc, vc = dev(kc0), dev(vc0)
     qn, o = empty(H * d), empty(H * d)
     ws = ops.Workspace(H, Hkv, d, maxk)
-    ops.decode_layer(dev(q), dev(k), dev(v), dev(gq), dev(gk), dev(inv), EPS, "neox", qn, kc, vc,
-                     o, pos, H, Hkv, d, maxk, ws)
+    ops.decode_layer(dev(q), dev(k), dev(v), dev(gq), dev(gk), dev(inv), EPS, pairing, qn, kc,
+                     vc, o, pos, H, Hkv, d, maxk, ws)
     got_o, got_qn = get(o, H * d), qn.download(H * d)
     got_kc, got_vc = kc.download(maxk * Hkv * d), vc.download(maxk * Hkv * d)
     kco, vco = kc0.copy(), vc0.copy()
-    want_qn, want_o = oracle.layer_attn_decode(q, k, v, gq, gk, inv, kco, vco, pos, H, Hkv, d)
+    want_qn, want_o = oracle.layer_attn_decode(q, k, v, gq, gk, inv, kco, vco, pos, H, Hkv, d,
+                                               pairing=pairing)
     assert np.array_equal(got_qn, want_qn)
     assert np.array_equal(got_kc, kco) and np.array_equal(got_vc, vco)
+    m = metrics(got_o, want_o, cf.attention(want_qn, kco, vco, H, Hkv, d, 1, pos))
+    assert meets_bar(m), fmt(m)
+    assert np.array_equal(argmax_rows(got_o, H), argmax_rows(want_o, H)), top2_margin(want_o, H)
+
+
+@pytest.mark.parametrize("n_keys_dev", [0, 1025, 5000])
+def test_decode_layer_dev_rejects_a_bad_position_on_the_device(rng, n_keys_dev):
+    # flk_decode_layer_dev reads the key count from device memory, where no
+    # host guard sees it. Past max_keys (the reference's "KV cache full",
+    # layer.ts:575) or 0, the kernel appends nothing, leaves qn as it was and
+    # fills o with NaN; the cache is unchanged.
+    H, Hkv, d, maxk = 16, 8, 128, 1024
+    kc0, vc0 = randn(rng, maxk * Hkv * d), randn(rng, maxk * Hkv * d)
+    q, k, v = randn(rng, H * d), randn(rng, Hkv * d), randn(rng, Hkv * d)
+    gq = rng.normal(1, 0.1, d).astype(np.float32)
+    gk = rng.normal(1, 0.1, d).astype(np.float32)
+    inv = ops.rope_inv_freq(d, 1e6)
+    kc, vc = dev(kc0), dev(vc0)
+    qn0 = np.full(H * d, 5.0, np.float32)
+    qn, o = dev(qn0), empty(H * d)
+    nk = ops.DeviceBuffer.from_array(np.array([n_keys_dev], np.uint32))
+    ws = ops.Workspace(H, Hkv, d, maxk)
+    ops.decode_layer_dev(dev(q), dev(k), dev(v), dev(gq), dev(gk), dev(inv), EPS, "neox", qn, kc,
+                         vc, o, nk, H, Hkv, d, maxk, ws)
+    ops.sync()
+    assert np.isnan(get(o, H * d)).all()
+    assert np.array_equal(qn.download(H * d), qn0)
+    assert np.array_equal(kc.download(maxk * Hkv * d), kc0)
+    assert np.array_equal(vc.download(maxk * Hkv * d), vc0)
+    # A valid count right after runs normally (nothing stuck from the bad call).
+    nk.upload(np.array([maxk], np.uint32))
+    ops.decode_layer_dev(dev(q), dev(k), dev(v), dev(gq), dev(gk), dev(inv), EPS, "neox", qn, kc,
+                         vc, o, nk, H, Hkv, d, maxk, ws)
+    got_o = get(o, H * d)
+    kco, vco = kc0.copy(), vc0.copy()
+    _, want_o = oracle.layer_attn_decode(q, k, v, gq, gk, inv, kco, vco, maxk - 1, H, Hkv, d)
+    assert np.array_equal(kc.download(maxk * Hkv * d), kco)
     m = metrics(got_o, want_o)
     assert meets_bar(m), fmt(m)
 
