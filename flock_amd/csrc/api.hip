@@ -8,6 +8,8 @@
 #include <stdio.h>
 #include <string.h>
 
+#include <mutex>
+
 #include "common.hpp"
 
 namespace flk {
@@ -319,13 +321,51 @@ int32_t flk_attn_prefill(const float* q, const float* kcache, const float* vcach
                     "flk_attn_prefill");
 }
 
+}  // extern "C"
+
+// ---------------------------------------------------- static split-K scratch ---
+// flk_decode_layer_noalloc takes its split-K partials from this array instead
+// of a caller workspace, for callers that cannot allocate. Every device the
+// library runs on holds its own copy until the process ends. Host code never
+// passes the array's name to a kernel (on the host it is only a stand-in):
+// the device address comes from hipGetSymbolAddress, once per device, with
+// that device current.
+constexpr uint64_t kScratchBytes = 8ull << 20;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+
+constexpr int kScratchDevices = 64;
+static void* g_scratch_ptr[kScratchDevices];
+static std::mutex g_scratch_mu;
+
+// Device address of the current device's scratch array.
+static int32_t scratch_ptr(void** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return hip_status(e, "hipGetDevice");
+  if (dev < 0 || dev >= kScratchDevices)
+    return fail(FLK_ERR_UNSUPPORTED, "device %d: static scratch is kept for devices 0..%d", dev,
+                kScratchDevices - 1);
+  std::lock_guard<std::mutex> lock(g_scratch_mu);
+  if (g_scratch_ptr[dev] == nullptr) {
+    void* p = nullptr;
+    e = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    if (e != hipSuccess) return hip_status(e, "hipGetSymbolAddress(scratch)");
+    g_scratch_ptr[dev] = p;
+  }
+  *out = g_scratch_ptr[dev];
+  return FLK_OK;
+}
+
+// ws == nullptr with use_scratch: the partials go to the static scratch array
+// (after every argument check has passed).
 static int32_t decode_layer_common(const float* q_raw, const float* k_raw, const float* v_raw,
                                    const float* gq, const float* gk, const float* inv_freq,
                                    float eps, int32_t pairing, float* qn_out, float* kcache,
                                    float* vcache, float* o, uint32_t n_keys,
                                    const uint32_t* n_keys_dev, uint32_t n_heads,
                                    uint32_t n_kv_heads, uint32_t head_dim, void* ws,
-                                   uint64_t ws_bytes, const char* what) {
+                                   uint64_t ws_bytes, const char* what,
+                                   bool use_scratch = false) {
   FLK_NONNULL(q_raw);
   FLK_NONNULL(k_raw);
   FLK_NONNULL(v_raw);
@@ -348,7 +388,21 @@ static int32_t decode_layer_common(const float* q_raw, const float* k_raw, const
   if (pairing != FLK_ROPE_NEOX && pairing != FLK_ROPE_NORM)
     return fail(FLK_ERR_ARG, "rope pairing %d (0 = neox, 1 = norm)", pairing);
   const DecodeShape s{n_heads, n_kv_heads, head_dim, 1, n_keys};
-  rc = check_ws(ws, ws_bytes, decode_ws_bytes(s));
+  const uint64_t need = decode_ws_bytes(s);
+  if (use_scratch) {
+    if (need > kScratchBytes)
+      return fail(FLK_ERR_WORKSPACE,
+                  "%s: %u heads over %u keys need %llu bytes of split-K scratch; the static "
+                  "scratch holds %llu (use flk_decode_layer with a workspace)",
+                  what, n_heads, n_keys, (unsigned long long)need,
+                  (unsigned long long)kScratchBytes);
+    ws_bytes = kScratchBytes;
+    if (need > 0) {
+      rc = scratch_ptr(&ws);
+      if (rc) return rc;
+    }
+  }
+  rc = check_ws(ws, ws_bytes, need);
   if (rc) return rc;
   DecodeFused f;
   f.q_raw = q_raw;
@@ -367,6 +421,8 @@ static int32_t decode_layer_common(const float* q_raw, const float* k_raw, const
                     what);
 }
 
+extern "C" {
+
 int32_t flk_decode_layer(const float* q_raw, const float* k_raw, const float* v_raw,
                          const float* gq, const float* gk, const float* inv_freq, float eps,
                          int32_t pairing, float* qn_out, float* kcache, float* vcache, float* o,
@@ -376,6 +432,17 @@ int32_t flk_decode_layer(const float* q_raw, const float* k_raw, const float* v_
   return decode_layer_common(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
                              vcache, o, pos + 1, nullptr, n_heads, n_kv_heads, head_dim, ws,
                              ws_bytes, "flk_decode_layer");
+}
+
+int32_t flk_decode_layer_noalloc(const float* q_raw, const float* k_raw, const float* v_raw,
+                                 const float* gq, const float* gk, const float* inv_freq,
+                                 float eps, int32_t pairing, float* qn_out, float* kcache,
+                                 float* vcache, float* o, uint32_t pos, uint32_t n_heads,
+                                 uint32_t n_kv_heads, uint32_t head_dim, uint32_t max_keys) {
+  if (pos >= max_keys) return fail(FLK_ERR_CACHE_FULL, "KV cache full at %u keys", max_keys);
+  return decode_layer_common(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
+                             vcache, o, pos + 1, nullptr, n_heads, n_kv_heads, head_dim, nullptr,
+                             0, "flk_decode_layer_noalloc", true);
 }
 
 int32_t flk_decode_layer_dev(const float* q_raw, const float* k_raw, const float* v_raw,

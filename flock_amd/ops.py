@@ -219,6 +219,18 @@ def decode_layer(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps: float, pairing, qn_
                                  max_keys, w, nb), "flk_decode_layer")
 
 
+def decode_layer_noalloc(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps: float, pairing, qn_out,
+                         kcache, vcache, o, pos: int, n_heads: int, n_kv_heads: int,
+                         head_dim: int, max_keys: int) -> None:
+    """flk_decode_layer without a workspace: the library's static scratch holds
+    the split-K partials (no allocation; calls on one device must not overlap)."""
+    check(lib().flk_decode_layer_noalloc(ptr(q_raw), ptr(k_raw), ptr(v_raw), ptr(gq), ptr(gk),
+                                         ptr(inv_freq), eps, _pairing(pairing), ptr(qn_out),
+                                         ptr(kcache), ptr(vcache), ptr(o), pos, n_heads,
+                                         n_kv_heads, head_dim, max_keys),
+          "flk_decode_layer_noalloc")
+
+
 def decode_layer_dev(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps: float, pairing, qn_out, kcache,
                      vcache, o, n_keys_dev, n_heads: int, n_kv_heads: int, head_dim: int,
                      max_keys: int, ws) -> None:

@@ -175,6 +175,23 @@ int32_t flk_decode_layer(const float* q_raw, const float* k_raw, const float* v_
                          float* o, uint32_t pos, uint32_t n_heads, uint32_t n_kv_heads,
                          uint32_t head_dim, uint32_t max_keys, void* ws, uint64_t ws_bytes);
 
+/* No counterpart in the reference. For callers that cannot allocate (code
+ * under graph capture, serving loops, harnesses that forbid hipMalloc):
+ * flk_decode_layer with no workspace argument. The split-K partials go to a
+ * static scratch array of 8 MiB that the library holds on each device until
+ * the process ends; a call needing more (flk_call_workspace_bytes(
+ * FLK_CALL_DECODE, ..., pos + 1, ...) > 8 MiB, i.e. more than ~63 heads of
+ * width 128) returns FLK_ERR_WORKSPACE before any launch. Nothing in the
+ * array must start at zero: each call's split kernel writes every partial
+ * its merge reads. All calls on one device share the array, so calls that
+ * overlap on one device (several streams or threads) race: order them on
+ * one stream. Same results as flk_decode_layer, bit for bit. */
+int32_t flk_decode_layer_noalloc(const float* q_raw, const float* k_raw, const float* v_raw,
+                                 const float* gq, const float* gk, const float* inv_freq,
+                                 float eps, int32_t pairing, float* qn_out, float* kcache,
+                                 float* vcache, float* o, uint32_t pos, uint32_t n_heads,
+                                 uint32_t n_kv_heads, uint32_t head_dim, uint32_t max_keys);
+
 /* Extension, no reference counterpart (the reference runs one sequence per
  * Layer, layer.ts:203-204): decode for n_seqs independent sequences in one
  * launch. q, o: [n_seqs][n_heads][head_dim]. Sequence b's cache rows start at

@@ -213,3 +213,16 @@ def test_dropped_buffers_are_freed_at_sync_not_on_collection():
     del b
     assert ops._pending_free == before + [FAKE]
     ops._pending_free.remove(FAKE)
+
+
+def test_noalloc_decode_rejects_calls_beyond_its_static_scratch():
+    # 64 heads of width 128 over 100000 keys need 256 splits x 64 heads x 520
+    # B = 8.5 MB of partials, above the 8 MiB static array: refused before any
+    # device call (there is no GPU here to reach).
+    L = _lib.lib()
+    rc, msg = code_and_msg(L.flk_decode_layer_noalloc(*([FAKE] * 6), 1e-6, 0, *([FAKE] * 4),
+                                                      99999, 64, 8, 128, 100000))
+    assert rc == _lib.FLK_ERR_WORKSPACE and "static scratch" in msg
+    rc, msg = code_and_msg(L.flk_decode_layer_noalloc(*([FAKE] * 6), 1e-6, 0, *([FAKE] * 4),
+                                                      2048, 16, 8, 128, 2048))
+    assert rc == _lib.FLK_ERR_CACHE_FULL
