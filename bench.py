@@ -42,11 +42,20 @@ of the hot path over one batch of synthetic, HBM-resident input:
   replay32k  Chunked replay: a 64-id chunk at position 32768 through Model.step
              (28 layers of prefill onto the cache + head). tokens/s.
 
-The default run also measures prefill2k (the metric's second half) and reports
-it under "prefill", the LM-head projection under "q8_lm_head", whole-model
-greedy generation at 32k context (gen32k) under "generate" and the 2048-token
-prompt (prompt2k) under "prompt". Inputs are N(0, 1) from a seeded generator
-(gains N(1, 0.1)); caches are written on the device before timing starts.
+The default run also measures, each under its own key with its own roofline:
+prefill2k ("prefill", the metric's second half), decode512 ("decode512"),
+ragged ("ragged"), chunk32k ("chunk32k", in TFLOP/s and in GB/s of K/V
+read), the LM-head projection ("q8_lm_head"),
+greedy generation at 32k context ("generate") and the 2048-token prompt
+("prompt"). Inputs are N(0, 1) from a seeded generator (gains N(1, 0.1));
+caches are written on the device before timing starts.
+
+CPU baselines (after every GPU measurement): the oracle (oracle/, C) on a
+bounded sample of the same workload, 1 thread (value, cores 1) and OpenMP on
+the host's share of cores ("openmp"), with the host's CPU model and nproc.
+Decode at 32k runs the whole 28-layer step once on 1 thread; prefill2k and
+ragged run in full; chunk32k runs one of its 28 layers and states the x28
+extrapolation.
 
 Timing: HIP events recorded on the stream the kernels are launched on bracket
 the K timed steps (after a synchronize). The roofline's average call duration
@@ -72,9 +81,12 @@ sys.path.insert(0, ROOT)
 METRIC = "decode-attn HBM GB/s (% peak) @32k ctx; prefill-attn TFLOP/s (% MFMA peak) @2k"
 HBM_PEAK_GBS = 8000.0          # MI355X HBM3E
 FP32_MFMA_PEAK_TFLOPS = 157.3  # MI355X dense fp32 matrix
-# MI355X published fp32 vector peak. It counts packed-fp32 instructions, which
-# this library never emits, so 78.6 TFLOP/s is the ceiling its VALU code can reach.
+# MI355X's published fp32 vector peak; VALU rooflines divide by it. It counts
+# packed-fp32 instructions (two flops per lane per cycle), which this library
+# never emits, so its VALU code can reach at most half of it: VALU rooflines
+# also report the fraction of that unpacked ceiling.
 FP32_VECTOR_PEAK_TFLOPS = 157.3
+FP32_UNPACKED_VALU_TFLOPS = 78.6
 H, HKV, D = 16, 8, 128
 EPS = 9.999999974752427e-7
 PROFILES = os.path.join(ROOT, "profiles")
@@ -118,18 +130,79 @@ class Workload:
         if self.bound == "hbm":
             achieved = self.work_per_call / (call_ms * 1e-3) / 1e9
             peak, unit, key = HBM_PEAK_GBS, "GB/s", "bytes_per_launch"
-        elif self.bound == "valu":
+        elif self.bound in ("valu", "mixed"):
             achieved = self.work_per_call / (call_ms * 1e-3) / 1e12
             peak, unit, key = FP32_VECTOR_PEAK_TFLOPS, "TFLOP/s", "flops_per_launch"
         else:
             achieved = self.work_per_call / (call_ms * 1e-3) / 1e12
             peak, unit, key = FP32_MFMA_PEAK_TFLOPS, "TFLOP/s", "flops_per_launch"
-        return {"bound": self.bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-                "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": self.kernel,
-                key: self.work_per_call, "avg_launch_us": round(call_ms * 1e3, 2)}
+        out = {"bound": self.bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+               "frac": round(achieved / peak, 4), "traffic": traffic, "kernel": self.kernel,
+               key: self.work_per_call, "avg_launch_us": round(call_ms * 1e3, 2)}
+        if self.bound in ("valu", "mixed"):
+            out["frac_of_unpacked_valu"] = round(achieved / FP32_UNPACKED_VALU_TFLOPS, 4)
+        if self.bound == "mixed":
+            out["note"] = ("flops of fp32-MFMA attention and VALU projections together, against "
+                           "the fp32 vector peak")
+        return out
+
+    # CPU baseline: cpu_sample(threads) runs a bounded sample of the same
+    # workload through the oracle and returns (work done, seconds, what ran).
+    cpu_sample = None
+    cpu_parallel = True
 
     def cpu_baseline(self):
-        return None
+        """The oracle on this host's cores: 1 thread (the primary figure, as the
+        reference's single-threaded TypeScript oracle), then OpenMP on the
+        host's share of cores."""
+        if self.cpu_sample is None:
+            return None
+        import oracle
+        model, nproc, share = cpu_info()
+        scale = 1e9 if self.unit == "GB/s" else 1e12
+        out = None
+        for th in (1, share):
+            oracle.set_threads(th)
+            work, dt, what = self.cpu_sample(th)
+            entry = {"value": round(work / dt / scale, 6), "unit": self.unit, "cores": th,
+                     "kind": "port", "sample": f"{what}; f32, {th} thread(s), {dt:.1f} s"}
+            if out is None:
+                out = dict(entry, nproc=nproc, cpu_model=model)
+            else:
+                out["openmp"] = entry
+            if share == 1 or not self.cpu_parallel:
+                break
+        oracle.set_threads(1)
+        return out
+
+
+def cpu_info():
+    """(CPU model, logical CPUs, threads for the all-cores leg). The threads
+    are the host's share for this GPU (OMP_NUM_THREADS when set), at most 16."""
+    model = ""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    model = line.split(":", 1)[1].strip()
+                    break
+    except OSError:
+        pass
+    nproc = os.cpu_count() or 1
+    share = int(os.environ.get("OMP_NUM_THREADS", "0") or 0) or nproc
+    return model, nproc, max(1, min(share, nproc, 16))
+
+
+def timed(fn, min_seconds, reps=None):
+    """Run fn() exactly `reps` times, or (reps None) until min_seconds have
+    passed, at least once; returns (reps, seconds)."""
+    n, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        n += 1
+        dt = time.perf_counter() - t0
+        if (reps is not None and n >= reps) or (reps is None and dt >= min_seconds):
+            return n, dt
 
 
 class Decode32k(Workload):
@@ -177,10 +250,11 @@ class Decode32k(Workload):
                 "layers": self.L, "n_keys": self.nk, "n_heads": H, "n_kv_heads": HKV,
                 "head_dim": D, "batch": 1, "kv_cache_bytes": 2 * self.L * self.maxk * HKV * D * 4}
 
-    def cpu_baseline(self, seconds=12.0):
-        """The oracle's attention slice of one layer (1 thread), repeated."""
+    def cpu_sample(self, threads):
+        """oracle layer_attn_decode (norm, RoPE, append, attention) of whole
+        layers: 1 thread, one layer per layer of the step (the full step, on
+        one host cache); more threads, repeated for >= 3 s."""
         import oracle
-        oracle.set_threads(1)
         rng = np.random.default_rng(5)
         nk = self.nk
         kc = rng.standard_normal(nk * HKV * D, dtype=np.float32)
@@ -189,19 +263,15 @@ class Decode32k(Workload):
         gq = rng.normal(1, 0.1, D).astype(np.float32)
         gk = rng.normal(1, 0.1, D).astype(np.float32)
         inv = oracle.rope_inv_freq(D)
-        oracle.layer_attn_decode(q, k, v, gq, gk, inv, kc, vc, nk - 1, H, HKV, D)  # warm-up
-        n, t0 = 0, time.perf_counter()
-        while True:
-            oracle.layer_attn_decode(q, k, v, gq, gk, inv, kc, vc, nk - 1, H, HKV, D)
-            n += 1
-            if time.perf_counter() - t0 > seconds:
-                break
-        dt = time.perf_counter() - t0
-        return {"value": round(n * self.work_per_call / dt / 1e9, 3), "unit": "GB/s",
-                "cores": 1, "kind": "port",
-                "sample": f"{n} x one layer of this workload (oracle layer_attn_decode: norm, "
-                          f"RoPE, append, attention over {nk} keys; f32, 1 thread): "
-                          f"{dt / n * 1e3:.1f} ms per layer, {dt:.1f} s total"}
+        layer = lambda: oracle.layer_attn_decode(q, k, v, gq, gk, inv, kc, vc, nk - 1, H, HKV, D)
+        layer()  # warm-up (page in the cache)
+        if threads == 1 and self.L > 1:
+            n, dt = timed(layer, 0.0, reps=self.L)
+            what = f"oracle layer_attn_decode x {n} layers (one whole step) over {nk} keys"
+        else:
+            n, dt = timed(layer, 3.0)
+            what = f"oracle layer_attn_decode x {n} over {nk} keys"
+        return n * self.work_per_call, dt, what
 
 
 class Decode512(Decode32k):
@@ -261,13 +331,13 @@ class Prefill2k(Workload):
                 "layers": self.L, "n_queries": self.n, "pos0": self.pos0, "n_heads": H,
                 "n_kv_heads": HKV, "head_dim": D}
 
-    def cpu_baseline(self, seconds=10.0):
-        """The oracle's prefill slice on a bounded prefix of the prompt (1 thread)."""
+    def cpu_sample(self, threads):
+        """oracle layer_attn_prefill (norm, RoPE, append, causal attention) of
+        one layer at the workload's full size, once; more threads, repeated
+        for >= 2 s."""
         import oracle
-        oracle.set_threads(1)
         rng = np.random.default_rng(6)
-        n = min(self.n, 384)
-        pos0 = self.pos0
+        n, pos0 = self.n, self.pos0
         nk = pos0 + n
         kc = np.zeros(nk * HKV * D, np.float32)
         vc = np.zeros_like(kc)
@@ -277,20 +347,13 @@ class Prefill2k(Workload):
         gq = rng.normal(1, 0.1, D).astype(np.float32)
         gk = rng.normal(1, 0.1, D).astype(np.float32)
         inv = oracle.rope_inv_freq(D)
-        flops = 4 * H * D * (n * pos0 + n * (n + 1) // 2)
-        reps, t0 = 0, time.perf_counter()
-        while True:
-            oracle.layer_attn_prefill(q, k, v, gq, gk, inv, kc.copy(), vc.copy(), n, pos0, H,
-                                      HKV, D)
-            reps += 1
-            if time.perf_counter() - t0 > seconds:
-                break
-        dt = time.perf_counter() - t0
-        return {"value": round(reps * flops / dt / 1e12, 6), "unit": "TFLOP/s", "cores": 1,
-                "kind": "port",
-                "sample": f"{reps} x oracle layer_attn_prefill of the first {n} tokens at "
-                          f"position {pos0} (norm, RoPE, append, attention; f32, 1 thread), "
-                          f"{dt:.1f} s"}
+        layer = lambda: oracle.layer_attn_prefill(q, k, v, gq, gk, inv, kc, vc, n, pos0, H, HKV, D)
+        reps, dt = timed(layer, 0.0 if threads == 1 else 2.0)
+        what = (f"oracle layer_attn_prefill x {reps}: {n} tokens at position {pos0}, one layer "
+                f"of {self.L}")
+        if self.L > 1:
+            what += f" (the {self.L}-layer step extrapolates to {dt / reps * self.L:.1f} s)"
+        return reps * self.work_per_call, dt, what
 
 
 class Chunk32k(Prefill2k):
@@ -299,6 +362,15 @@ class Chunk32k(Prefill2k):
 
     def __init__(self, torch, ops):
         super().__init__(torch, ops, n=64, pos0=32768, layers=28)
+        # Bytes an attention call must move: every K and V row of the cache
+        # (pos0 + n keys, 8 kv heads) once, q in and o out.
+        self.bytes_per_call = (2 * self.maxk * HKV * D * 4) + 2 * self.n * H * D * 4
+
+    def extra(self, ms, call_ms):
+        return {"hbm": {"bytes_per_launch": self.bytes_per_call,
+                        "achieved": round(self.bytes_per_call / (call_ms * 1e-3) / 1e9, 2),
+                        "unit": "GB/s", "peak": HBM_PEAK_GBS,
+                        "frac": round(self.bytes_per_call / (call_ms * 1e-3) / 1e9 / HBM_PEAK_GBS, 4)}}
 
 
 class Ragged(Workload):
@@ -337,26 +409,25 @@ class Ragged(Workload):
                             f"(sum {self.rows})", "n_seqs": self.B, "sum_n_keys": self.rows,
                 "n_heads": H, "n_kv_heads": HKV, "head_dim": D}
 
-    def cpu_baseline(self, seconds=10.0):
-        """oracle.attn over the batch's sequence lengths, in order, for ~10 s."""
+    def cpu_sample(self, threads):
+        """oracle attn over every sequence of the batch in order (one host cache
+        of the longest length, sliced per sequence); more threads, the batch
+        repeated for >= 2 s."""
         import oracle
-        oracle.set_threads(1)
         rng = np.random.default_rng(8)
         longest = int(self.n_keys.max())
         kc = rng.standard_normal(longest * HKV * D, dtype=np.float32)
         vc = rng.standard_normal(longest * HKV * D, dtype=np.float32)
         q = rng.standard_normal(H * D, dtype=np.float32)
-        done_rows, n, t0 = 0, 0, time.perf_counter()
-        while time.perf_counter() - t0 < seconds:
-            nk = int(self.n_keys[n % self.B])
-            oracle.attn(q, kc[:nk * HKV * D], vc[:nk * HKV * D], H, HKV, D, nk)
-            done_rows += nk
-            n += 1
-        dt = time.perf_counter() - t0
-        return {"value": round((2 * done_rows * HKV * D * 4 + 2 * n * H * D * 4) / dt / 1e9, 3),
-                "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"oracle attn over the first {n} of the batch's sequences "
-                          f"({done_rows} keys; f32, 1 thread), {dt:.1f} s"}
+
+        def batch():
+            for nk in self.n_keys:
+                nk = int(nk)
+                oracle.attn(q, kc[:nk * HKV * D], vc[:nk * HKV * D], H, HKV, D, nk)
+
+        reps, dt = timed(batch, 0.0 if threads == 1 else 2.0)
+        return reps * self.work_per_call, dt, (f"oracle attn over all {self.B} sequences "
+                                               f"({self.rows} keys) x {reps}")
 
 
 class Copy(Workload):
@@ -420,8 +491,9 @@ class Q8LmHead(Workload):
         return {"workload": f"Q8_0 matvec {self.rows} x {self.cols} (LM head), 1 token",
                 "rows": self.rows, "cols": self.cols, "weight_bytes": self.rows * self.cols * 34 // 32}
 
-    def cpu_baseline(self, seconds=10.0):
-        """oracle.q8_matvec (coop(64), 1 thread) on 4096-row slices, ~10 s."""
+    def cpu_sample(self, threads):
+        """oracle.q8_matvec (coop(64); a serial loop, so 1 thread) on 4096-row
+        slices of the head for >= 5 s."""
         import oracle
         rng = np.random.default_rng(9)
         rows = 4096
@@ -431,15 +503,11 @@ class Q8LmHead(Workload):
         blocks[:, 2:] = rng.integers(0, 256, (blocks.shape[0], 32), dtype=np.uint8)
         packed = blocks.ravel()
         x = rng.standard_normal(self.cols).astype(np.float32)
-        n, t0 = 0, time.perf_counter()
-        while time.perf_counter() - t0 < seconds:
-            oracle.q8_matvec(packed, x, rows, self.cols, 64)
-            n += 1
-        dt = time.perf_counter() - t0
+        n, dt = timed(lambda: oracle.q8_matvec(packed, x, rows, self.cols, 64), 5.0)
         per = rows * self.cols * 34 // 32 + 4 * (self.cols + rows)
-        return {"value": round(n * per / dt / 1e9, 3), "unit": "GB/s", "cores": 1, "kind": "port",
-                "sample": f"{n} x oracle q8_matvec of a {rows} x {self.cols} slice (coop(64), "
-                          f"1 thread), {dt:.1f} s"}
+        return n * per, dt, f"oracle q8_matvec of a {rows} x {self.cols} slice x {n}"
+
+    cpu_parallel = False  # the q8 oracle has no parallel loop
 
 
 class Q8Proj(Workload):
@@ -553,7 +621,7 @@ class Prompt2k(Workload):
 
     name = "prompt2k"
     unit = "tokens/s"
-    bound = "valu"
+    bound = "mixed"
     kernel = "Model.step(2048 ids): embed, 28 x encodePrefill, lm_head"
     n_tokens = 2048
 
@@ -593,7 +661,7 @@ class Prompt2k(Workload):
     def step(self):
         self.call()
 
-    def extra(self, ms):
+    def extra(self, ms, call_ms):
         return {"ms_per_prompt": round(ms, 3)}
 
     def config(self):
@@ -651,7 +719,7 @@ class Replay32k(Prompt2k):
             layer.nKeys = self.n_keys
         m.step(self.ids)
 
-    def extra(self, ms):
+    def extra(self, ms, call_ms):
         return {"ms_per_chunk": round(ms, 3)}
 
     def config(self):
@@ -725,7 +793,7 @@ class Token(Workload):
     def step(self):
         self.call()
 
-    def extra(self, ms):
+    def extra(self, ms, call_ms):
         return {"tokens_per_s": round(1e3 / ms, 2), "ms_per_token": round(ms, 4)}
 
     def config(self):
@@ -804,7 +872,7 @@ class Gen(Workload):
     def step(self):
         self.call()
 
-    def extra(self, ms):
+    def extra(self, ms, call_ms):
         return {"tokens_per_s": round(self.tokens * 1e3 / ms, 2),
                 "ms_per_token": round(ms / self.tokens, 4)}
 
@@ -881,7 +949,7 @@ def run(torch, ops, stream, name, steps, warmup):
            "data": w.data, "config": w.config(),
            "roofline": w.roofline(call_ms, traffic_from_profiles(f"{name}_pmc.md"))}
     if hasattr(w, "extra"):
-        out.update(w.extra(ms))
+        out.update(w.extra(ms, call_ms))
     # Drop the device buffers; the CPU baseline needs only the sizes.
     if hasattr(w, "model"):
         w.model.free()
@@ -901,8 +969,8 @@ def main():
     ap.add_argument("--workload", default="decode32k", choices=sorted(WORKLOADS))
     ap.add_argument("--no-cpu-baseline", action="store_true")
     ap.add_argument("--no-secondary", action="store_true",
-                    help="skip the prefill2k, q8lmhead, gen32k and prompt2k measurements of the "
-                         "default run")
+                    help="measure only the main workload (the default run also measures "
+                         "prefill2k, decode512, ragged, chunk32k, q8lmhead, gen32k, prompt2k)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) != 1:
@@ -939,29 +1007,35 @@ def main():
         for k in ("ms_per_prompt", "ms_per_chunk"):
             if k in main_res:
                 out[k] = main_res[k]
-        pre_cpu = q8_cpu = None
+        # The other benchmark workloads and the rows next to the path,
+        # each with its own roofline (and CPU baseline where it has one).
+        secondary = []
         if args.workload == "decode32k" and not args.no_secondary:
-            p, pre_cpu = run(torch, ops, stream, "prefill2k", max(5, args.steps), args.warmup)
-            p["frac_of_fp32_mfma_peak"] = round(p["value"] / FP32_MFMA_PEAK_TFLOPS, 4)
-            out["prefill"] = p
-            q, q8_cpu = run(torch, ops, stream, "q8lmhead", max(5, args.steps), args.warmup)
-            q["frac_of_hbm_peak"] = round(q["value"] / HBM_PEAK_GBS, 4)
-            out["q8_lm_head"] = q
-            g, _ = run(torch, ops, stream, "gen32k", 5, 2)
-            g["frac_of_hbm_peak"] = round(g["value"] / HBM_PEAK_GBS, 4)
-            out["generate"] = g
-            t, _ = run(torch, ops, stream, "prompt2k", 3, 1)
-            out["prompt"] = t
+            for key, name, steps, warm in (
+                    ("prefill", "prefill2k", max(5, args.steps), args.warmup),
+                    ("decode512", "decode512", max(20, args.steps), args.warmup),
+                    ("ragged", "ragged", max(5, args.steps // 2), args.warmup),
+                    ("chunk32k", "chunk32k", max(5, args.steps // 2), args.warmup),
+                    ("q8_lm_head", "q8lmhead", max(5, args.steps), args.warmup),
+                    ("generate", "gen32k", 5, 2),
+                    ("prompt", "prompt2k", 3, 1)):
+                res, cpu = run(torch, ops, stream, name, steps, warm)
+                b = res["roofline"]["bound"]
+                if res["unit"] == "GB/s":
+                    res["frac_of_hbm_peak"] = round(res["value"] / HBM_PEAK_GBS, 4)
+                elif res["unit"] == "TFLOP/s" and b == "mfma":
+                    res["frac_of_fp32_mfma_peak"] = round(res["value"] / FP32_MFMA_PEAK_TFLOPS, 4)
+                out[key] = res
+                secondary.append((key, name, cpu))
     # CPU baselines last, with the GPU measurements done.
     if not args.no_cpu_baseline:
-        log(f"[{args.workload}] CPU baseline (oracle port, 1 thread)")
+        log(f"[{args.workload}] CPU baseline (oracle port)")
         out["cpu_baseline"] = main_cpu()
-        if pre_cpu is not None:
-            log("[prefill2k] CPU baseline (oracle port, 1 thread)")
-            out["prefill"]["cpu_baseline"] = pre_cpu()
-        if q8_cpu is not None:
-            log("[q8lmhead] CPU baseline (oracle port, 1 thread)")
-            out["q8_lm_head"]["cpu_baseline"] = q8_cpu()
+        for key, name, cpu in secondary:
+            log(f"[{name}] CPU baseline (oracle port)")
+            cb = cpu()
+            if cb is not None:
+                out[key]["cpu_baseline"] = cb
     print(json.dumps(out), flush=True)
 
 

@@ -22,7 +22,7 @@ def pytest_configure(config):
 
 
 def _gpu_count() -> int:
-    """Visible GPUs, counted without our library: on a GPU box a missing or
+    """Visible GPUs, counted without our library: with a GPU present a missing or
     broken libflock_attn.so must fail the gpu tests, not skip them."""
     try:
         import torch
@@ -42,7 +42,7 @@ def pytest_collection_modifyitems(config, items):
 
 # ------------------------------------------------------------------ helpers --
 def randn(rng: np.random.Generator, n: int) -> np.ndarray:
-    """N(0, 1) values as f32 (the BASELINE configs' inputs)."""
+    """N(0, 1) values as f32 (the benchmark workloads' inputs)."""
     return rng.standard_normal(n, dtype=np.float32)
 
 

@@ -53,8 +53,33 @@ def meets_bar(m: dict) -> bool:
     return m["gpu_abs_vs_f64"] <= 2 * m["oracle_abs_vs_f64"] + 1e-7
 
 
+def clause(m: dict) -> str:
+    """Which part of the bar decided: 'literal' (max-abs 2e-5 and relErr
+    1e-4 both hold), '2x-oracle' (relErr above 1e-4, passed on the distance
+    from float64), or 'fail'."""
+    if m["max_abs"] > MAX_ABS:
+        return "fail"
+    if m["rel"] <= MAX_REL:
+        return "literal"
+    return "2x-oracle" if meets_bar(m) else "fail"
+
+
 def fmt(m: dict) -> str:
     return "  ".join(f"{k}={v:.2e}" for k, v in m.items())
+
+
+def record(case: str, m: dict, **extra) -> None:
+    """Print a case's parity numbers and, when FLK_PARITY_LOG names a file,
+    append them to it as one JSON line (the per-configuration parity table
+    is built from that file)."""
+    import json
+    import os
+    row = {"case": case, "clause": clause(m), **{k: float(v) for k, v in m.items()}, **extra}
+    print(json.dumps(row), flush=True)
+    path = os.environ.get("FLK_PARITY_LOG")
+    if path:
+        with open(path, "a") as f:
+            f.write(json.dumps(row) + "\n")
 
 
 def argmax_rows(x: np.ndarray, rows: int) -> np.ndarray:

@@ -176,7 +176,7 @@ def test_decode_reference_cases(rng, H, Hkv, nk):
 
 @pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("nk", [1, 2, 63, 64, 65, 513, 2049, 32769])
-def test_decode_north_star_bar(rng, d, nk):
+def test_decode_parity_bar_long_context(rng, d, nk):
     # N(0,1) inputs (the long-context configs' distribution), split-K in play
     # from a few hundred keys on.
     H, Hkv = 16, 8
