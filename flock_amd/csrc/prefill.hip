@@ -28,7 +28,10 @@
 // contiguous floats of a K row from LDS.
 //
 // Each tile's K/V rows are loaded into registers while the previous tile is
-// computed, then written to LDS. Causal bound: query at absolute position p
+// computed, then written to LDS. The loads go through a buffer descriptor
+// made per tile (scalar registers): a thread's offset within the tile is the
+// same for every tile, so the fetch costs no per-tile address arithmetic, and
+// rows past the last key read as 0. Causal bound: query at absolute position p
 // sees keys 0..p (attention_prefill.wgsl:90), applied per element.
 //
 // Scheduling (1-D grid, workgroup id = kv head + n_kv_heads * work item, so
@@ -76,57 +79,48 @@ __host__ __device__ __forceinline__ uint32_t qtile_kt(uint32_t qt, uint32_t q_pe
   return (pos0 + q_end + kBK - 1) / kBK;
 }
 
-__device__ __forceinline__ float4 mask4(float4 v, uint32_t keep) {
-  return make_float4(__uint_as_float(__float_as_uint(v.x) & keep),
-                     __uint_as_float(__float_as_uint(v.y) & keep),
-                     __uint_as_float(__float_as_uint(v.z) & keep),
-                     __uint_as_float(__float_as_uint(v.w) & keep));
-}
+// gfx9 buffer-descriptor word 3 for untyped 32-bit-element loads.
+constexpr int kBufferWord3 = 0x00020000;
 
-// K/V rows of key tile kt into registers: NPF float4 of each per thread.
-// Rows past the last key are loaded from the last key row (a valid address)
-// and zeroed when written to LDS.
+// K/V rows of key tile kt into registers: NPF float4 of each per thread. The
+// descriptors cover the tile's live rows only (rows from kt * kBK, at most
+// kBK, at most up to the last key), so a row past the last key reads as 0.
 template <int D, int NPF = kBK * D / 4 / kPThreads>
 __device__ __forceinline__ void load_tile(float4 (&pk)[NPF], float4 (&pv)[NPF],
                                           const PrefillArgs& a, uint32_t kvh, uint32_t kt,
                                           uint32_t n_keys_total, int tid) {
-  const size_t row = (size_t)a.n_kv_heads * D;
+  const uint32_t key0 = kt * kBK;
+  const uint32_t rows = min(n_keys_total - key0, (uint32_t)kBK);
+  const uint32_t row_bytes = a.n_kv_heads * D * 4;
+  const size_t base = (size_t)key0 * row_bytes + (size_t)kvh * D * 4;
+  const uint32_t n_bytes = (rows - 1) * row_bytes + D * 4;  // end of the last live row's head
+  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(reinterpret_cast<const char*>(a.kcache) + base), 0, n_bytes, kBufferWord3);
+  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(reinterpret_cast<const char*>(a.vcache) + base), 0, n_bytes, kBufferWord3);
+  typedef float f4v __attribute__((ext_vector_type(4)));
 #pragma unroll
   for (int i = 0; i < NPF; i++) {
     const int f = tid + kPThreads * i;
     const int r = f / (D / 4), c4 = f % (D / 4);
-    const uint32_t key = min(kt * kBK + r, n_keys_total - 1);
-    const size_t off = (size_t)key * row + (size_t)kvh * D + 4 * c4;
-    pk[i] = *reinterpret_cast<const float4*>(a.kcache + off);
-    pv[i] = *reinterpret_cast<const float4*>(a.vcache + off);
+    const int off = r * (int)row_bytes + 16 * c4;
+    const f4v k4 = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
+    const f4v v4 = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
+    pk[i] = make_float4(k4.x, k4.y, k4.z, k4.w);
+    pv[i] = make_float4(v4.x, v4.y, v4.z, v4.w);
   }
 }
 
-// Registers of key tile kt into one LDS buffer (K rows padded to D + 4).
-// Rows past the last key become zeros (a bit mask, not a select: the compiler
-// turns a select between two values into a select of their addresses, which
-// forces the prefetch registers into scratch).
+// Registers of one key tile into one LDS buffer (K rows padded to D + 4).
 template <int D, int NPF = kBK * D / 4 / kPThreads>
 __device__ __forceinline__ void store_tile(const float4 (&pk)[NPF], const float4 (&pv)[NPF],
-                                           float* k_lds, float* v_lds, uint32_t kt,
-                                           uint32_t n_keys_total, int tid) {
-  if ((kt + 1) * kBK <= n_keys_total) {  // uniform: every row of the tile is live
-#pragma unroll
-    for (int i = 0; i < NPF; i++) {
-      const int f = tid + kPThreads * i;
-      const int rr = f / (D / 4), c4 = f % (D / 4);
-      *reinterpret_cast<float4*>(&k_lds[rr * (D + 4) + 4 * c4]) = pk[i];
-      *reinterpret_cast<float4*>(&v_lds[rr * D + 4 * c4]) = pv[i];
-    }
-    return;
-  }
+                                           float* k_lds, float* v_lds, int tid) {
 #pragma unroll
   for (int i = 0; i < NPF; i++) {
     const int f = tid + kPThreads * i;
     const int rr = f / (D / 4), c4 = f % (D / 4);
-    const uint32_t keep = kt * kBK + rr < n_keys_total ? 0xffffffffu : 0u;
-    *reinterpret_cast<float4*>(&k_lds[rr * (D + 4) + 4 * c4]) = mask4(pk[i], keep);
-    *reinterpret_cast<float4*>(&v_lds[rr * D + 4 * c4]) = mask4(pv[i], keep);
+    *reinterpret_cast<float4*>(&k_lds[rr * (D + 4) + 4 * c4]) = pk[i];
+    *reinterpret_cast<float4*>(&v_lds[rr * D + 4 * c4]) = pv[i];
   }
 }
 
@@ -174,20 +168,24 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     const float4* src = reinterpret_cast<const float4*>(
         a.q + ((size_t)(row_ok ? qi : q0) * a.n_heads + (row_ok ? h : kvh * a.group)) * D +
         DS * lg);
+    // q is pre-multiplied by scale * log2(e), so S^T comes out in base-2 units.
 #pragma unroll
     for (int s4 = 0; s4 < DS / 4; s4++) {
       const float4 v = src[s4];
-      qreg[4 * s4 + 0] = v.x;
-      qreg[4 * s4 + 1] = v.y;
-      qreg[4 * s4 + 2] = v.z;
-      qreg[4 * s4 + 3] = v.w;
+      qreg[4 * s4 + 0] = v.x * a.scale_log2e;
+      qreg[4 * s4 + 1] = v.y * a.scale_log2e;
+      qreg[4 * s4 + 2] = v.z * a.scale_log2e;
+      qreg[4 * s4 + 3] = v.w * a.scale_log2e;
     }
   }
 
   floatx4 oacc[CB];
 #pragma unroll
   for (int c = 0; c < CB; c++) oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
-  float m_run = -INFINITY, l_run = 0.f;
+  // Running reference m_run (log2 units; finite, so that a masked key's
+  // weight exp2(-inf - m_run) is exactly 0) and this lane's share of the
+  // denominator (its keys only; summed over the row's lanes at the end).
+  float m_run = -1e30f, l_run = 0.f;
 
   // A tile needs no causal mask when its last key is at or before the q
   // tile's first query position and every row of the q tile is live.
@@ -198,7 +196,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   // tile kt + 1 is stored into the other one and tile kt + 2 loads into
   // registers; one barrier per tile separates the two.
   __syncthreads();  // LDS may still hold the previous q tile's merge data
-  store_tile<D>(pk, pv, k_lds, v_lds, kt0, n_keys_total, tid);
+  store_tile<D>(pk, pv, k_lds, v_lds, tid);
   load_tile<D>(pk, pv, a, kvh, kt0 + 1 < kt1 ? kt0 + 1 : kt0, n_keys_total, tid);
   __syncthreads();
 
@@ -249,8 +247,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
       // kt + 1 goes from registers into the other buffer and tile kt + 2 is
       // requested (the last one is simply loaded again at the end).
       if (g == NG / 2 && kt + 1 < kt1) {
-        store_tile<D>(pk, pv, k_lds + (buf ^ 1) * (kBK * LDK), v_lds + (buf ^ 1) * (kBK * D),
-                      kt + 1, n_keys_total, tid);
+        store_tile<D>(pk, pv, k_lds + (buf ^ 1) * (kBK * LDK), v_lds + (buf ^ 1) * (kBK * D), tid);
         load_tile<D>(pk, pv, a, kvh, kt + 2 < kt1 ? kt + 2 : kt + 1, n_keys_total, tid);
       }
       __builtin_amdgcn_sched_barrier(0);
@@ -272,54 +269,49 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     __builtin_amdgcn_sched_barrier(0);
 
     // ---- online softmax of this lane's row (base 2) ----------------------------
-    // Scores are kept as log2-scaled values t = (q.k) * scale * log2(e), so
-    // every exponential is one v_exp_f32; m_run is in the same units. Tiles
-    // wholly below the causal diagonal with every row live skip the mask.
-    float mx = -INFINITY;
-    if (full_tile(key0)) {
-#pragma unroll
-      for (int b = 0; b < kHalfKB; b++)
-#pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float t = sacc[b][i] * a.scale_log2e;
-          sacc[b][i] = t;
-          mx = fmaxf(mx, t);
-        }
-    } else {
+    // Scores are base-2 already (q carries scale * log2(e)), so every weight is
+    // one v_exp_f32 against the reference m_run. The reference moves only when
+    // some score of the wave exceeds it by more than 8 (a factor 256): the
+    // check needs only each lane's own 8 scores, and the row's maximum across
+    // its four lane groups is formed only then (rarely after the first tile).
+    // Otherwise the weights are taken against the old reference -- each at
+    // most 256 -- and nothing is rescaled. Tiles wholly below the causal
+    // diagonal with every row live skip the mask.
+    if (!full_tile(key0)) {
 #pragma unroll
       for (int b = 0; b < kHalfKB; b++)
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const uint32_t key = key0 + (half * kHalfKB + b) * 16 + 4 * lg + i;
-          const float t = (row_ok && key <= qpos) ? sacc[b][i] * a.scale_log2e : -INFINITY;
-          sacc[b][i] = t;
-          mx = fmaxf(mx, t);
+          if (!(row_ok && key <= qpos)) sacc[b][i] = -INFINITY;
         }
     }
-    mx = max_xor<16>(mx);
-    mx = max_xor<32>(mx);
-    const float mn = fmaxf(m_run, mx);
-    float corr = 1.f, rs = 0.f;
-    if (mn != -INFINITY) {
-      corr = __builtin_amdgcn_exp2f(m_run - mn);
+    float lmx = sacc[0][0];
 #pragma unroll
-      for (int b = 0; b < kHalfKB; b++)
+    for (int b = 0; b < kHalfKB; b++)
 #pragma unroll
-        for (int i = 0; i < 4; i++) {
-          const float p = __builtin_amdgcn_exp2f(sacc[b][i] - mn);
-          sacc[b][i] = p;
-          rs += p;
-        }
-    } else {
+      for (int i = 0; i < 4; i++) lmx = fmaxf(lmx, sacc[b][i]);
+    if (__builtin_amdgcn_ballot_w64(lmx > m_run + 8.f) != 0) {  // uniform branch
+      // Only rows whose own maximum passed the threshold move their reference;
+      // the others keep it and are multiplied by exactly 1, so a row's result
+      // depends on its own keys only (causality holds bit for bit).
+      float mx = max_xor<16>(lmx);
+      mx = max_xor<32>(mx);
+      const bool up = mx > m_run + 8.f;
+      const float corr = up ? __builtin_amdgcn_exp2f(m_run - mx) : 1.f;
+      l_run *= corr;
 #pragma unroll
-      for (int b = 0; b < kHalfKB; b++) sacc[b] = floatx4{0.f, 0.f, 0.f, 0.f};
+      for (int c = 0; c < CB; c++) oacc[c] *= corr;
+      m_run = up ? mx : m_run;
     }
-    rs = sum_xor<16>(rs);
-    rs = sum_xor<32>(rs);
-    l_run = l_run * corr + rs;
-    m_run = mn;
 #pragma unroll
-    for (int c = 0; c < CB; c++) oacc[c] *= corr;
+    for (int b = 0; b < kHalfKB; b++)
+#pragma unroll
+      for (int i = 0; i < 4; i++) {
+        const float p = __builtin_amdgcn_exp2f(sacc[b][i] - m_run);
+        sacc[b][i] = p;
+        l_run += p;
+      }
 
     // ---- O^T += V^T P^T ---------------------------------------------------------
 #pragma unroll
@@ -339,6 +331,8 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     __syncthreads();  // tile kt + 1 stored; buffer of tile kt free again
   }
 
+  l_run = sum_xor<16>(l_run);  // the row's denominator: its four lane groups
+  l_run = sum_xor<32>(l_run);
   // ---- combine the two key halves of each row through LDS --------------------
   // Lane holds channels 4*CB*lg + CB*j + c of its row. The upper waves park
   // their (m, l, acc) in the (now free) K tile buffer; the lower waves fold
@@ -363,8 +357,10 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   if (half == 1) return;
   const float m2 = m_lds[r], l2 = m_lds[kRows + r];
   const float M = fmaxf(m_run, m2);
-  const float w1 = m_run == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m_run - M);
-  const float w2 = m2 == -INFINITY ? 0.f : __builtin_amdgcn_exp2f(m2 - M);
+  // A half that saw no key of this row still holds the initial reference
+  // (-1e30, l = 0): its weight exp2(-1e30 - M) is 0.
+  const float w1 = __builtin_amdgcn_exp2f(m_run - M);
+  const float w2 = __builtin_amdgcn_exp2f(m2 - M);
   const float L = l_run * w1 + l2 * w2;
   const float* o2 = o_lds + r * D + 4 * CB * lg;
   float* dst;
