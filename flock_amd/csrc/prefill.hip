@@ -82,32 +82,55 @@ __host__ __device__ __forceinline__ uint32_t qtile_kt(uint32_t qt, uint32_t q_pe
 // gfx9 buffer-descriptor word 3 for untyped 32-bit-element loads.
 constexpr int kBufferWord3 = 0x00020000;
 
-// K/V rows of key tile kt into registers: NPF float4 of each per thread. The
-// descriptors cover the tile's live rows only (rows from kt * kBK, at most
-// kBK, at most up to the last key), so a row past the last key reads as 0.
+// Rows of key tile kt of `cache` (K or V) into registers: NPF float4 per
+// thread. The descriptor covers the tile's live rows only (rows from kt * kBK,
+// at most kBK, at most up to the last key), so a row past the last key reads
+// as 0.
 template <int D, int NPF = kBK * D / 4 / kPThreads>
-__device__ __forceinline__ void load_tile(float4 (&pk)[NPF], float4 (&pv)[NPF],
+__device__ __forceinline__ void load_rows(float4 (&pr)[NPF], const float* cache,
                                           const PrefillArgs& a, uint32_t kvh, uint32_t kt,
                                           uint32_t n_keys_total, int tid) {
   const uint32_t key0 = kt * kBK;
   const uint32_t rows = min(n_keys_total - key0, (uint32_t)kBK);
   const uint32_t row_bytes = a.n_kv_heads * D * 4;
   const size_t base = (size_t)key0 * row_bytes + (size_t)kvh * D * 4;
-  const uint32_t n_bytes = (rows - 1) * row_bytes + D * 4;  // end of the last live row's head
-  const __amdgpu_buffer_rsrc_t rk = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char*>(reinterpret_cast<const char*>(a.kcache) + base), 0, n_bytes, kBufferWord3);
-  const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char*>(reinterpret_cast<const char*>(a.vcache) + base), 0, n_bytes, kBufferWord3);
+  const uint32_t n_bytes = (rows - 1) * row_bytes + D * 4;
+  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
+      const_cast<char*>(reinterpret_cast<const char*>(cache) + base), 0, n_bytes, kBufferWord3);
   typedef float f4v __attribute__((ext_vector_type(4)));
 #pragma unroll
   for (int i = 0; i < NPF; i++) {
     const int f = tid + kPThreads * i;
     const int r = f / (D / 4), c4 = f % (D / 4);
-    const int off = r * (int)row_bytes + 16 * c4;
-    const f4v k4 = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rk, off, 0, 0));
-    const f4v v4 = __builtin_bit_cast(f4v, __builtin_amdgcn_raw_buffer_load_b128(rv, off, 0, 0));
-    pk[i] = make_float4(k4.x, k4.y, k4.z, k4.w);
-    pv[i] = make_float4(v4.x, v4.y, v4.z, v4.w);
+    const f4v x = __builtin_bit_cast(
+        f4v, __builtin_amdgcn_raw_buffer_load_b128(rr, r * (int)row_bytes + 16 * c4, 0, 0));
+    pr[i] = make_float4(x.x, x.y, x.z, x.w);
+  }
+}
+
+// K and V rows of key tile kt into registers.
+template <int D, int NPF = kBK * D / 4 / kPThreads>
+__device__ __forceinline__ void load_tile(float4 (&pk)[NPF], float4 (&pv)[NPF],
+                                          const PrefillArgs& a, uint32_t kvh, uint32_t kt,
+                                          uint32_t n_keys_total, int tid) {
+  load_rows<D>(pk, a.kcache, a, kvh, kt, n_keys_total, tid);
+  load_rows<D>(pv, a.vcache, a, kvh, kt, n_keys_total, tid);
+}
+
+template <int D, int NPF = kBK * D / 4 / kPThreads>
+__device__ __forceinline__ void store_k(const float4 (&pk)[NPF], float* k_lds, int tid) {
+#pragma unroll
+  for (int i = 0; i < NPF; i++) {
+    const int f = tid + kPThreads * i;
+    *reinterpret_cast<float4*>(&k_lds[(f / (D / 4)) * (D + 4) + 4 * (f % (D / 4))]) = pk[i];
+  }
+}
+template <int D, int NPF = kBK * D / 4 / kPThreads>
+__device__ __forceinline__ void store_v(const float4 (&pv)[NPF], float* v_lds, int tid) {
+#pragma unroll
+  for (int i = 0; i < NPF; i++) {
+    const int f = tid + kPThreads * i;
+    *reinterpret_cast<float4*>(&v_lds[(f / (D / 4)) * D + 4 * (f % (D / 4))]) = pv[i];
   }
 }
 
@@ -115,25 +138,51 @@ __device__ __forceinline__ void load_tile(float4 (&pk)[NPF], float4 (&pv)[NPF],
 template <int D, int NPF = kBK * D / 4 / kPThreads>
 __device__ __forceinline__ void store_tile(const float4 (&pk)[NPF], const float4 (&pv)[NPF],
                                            float* k_lds, float* v_lds, int tid) {
+  store_k<D>(pk, k_lds, tid);
+  store_v<D>(pv, v_lds, tid);
+}
+
+// This lane's row of q tile qt in the B-operand layout of S^T = K Q^T (D/4
+// floats from dim (D/4) * lg), pre-multiplied by scale * log2(e) so that S^T
+// comes out in base-2 units.
+template <int D>
+__device__ __forceinline__ void load_q(float (&qreg)[D / 4], const PrefillArgs& a, uint32_t kvh,
+                                       uint32_t qt) {
+  constexpr int DS = D / 4;
+  const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
+  const int lc = lane & 15, lg = lane >> 4;
+  const uint32_t q0 = qt * a.q_per_tile;
+  const uint32_t r = (wave & 3) * 16 + lc;
+  const uint32_t qi = q0 + r / a.group;
+  const uint32_t h = kvh * a.group + r % a.group;
+  const bool row_ok = r < a.q_per_tile * a.group && qi < a.n_queries;
+  const float4* src = reinterpret_cast<const float4*>(
+      a.q + ((size_t)(row_ok ? qi : q0) * a.n_heads + (row_ok ? h : kvh * a.group)) * D + DS * lg);
 #pragma unroll
-  for (int i = 0; i < NPF; i++) {
-    const int f = tid + kPThreads * i;
-    const int rr = f / (D / 4), c4 = f % (D / 4);
-    *reinterpret_cast<float4*>(&k_lds[rr * (D + 4) + 4 * c4]) = pk[i];
-    *reinterpret_cast<float4*>(&v_lds[rr * D + 4 * c4]) = pv[i];
+  for (int s4 = 0; s4 < DS / 4; s4++) {
+    const float4 v = src[s4];
+    qreg[4 * s4 + 0] = v.x * a.scale_log2e;
+    qreg[4 * s4 + 1] = v.y * a.scale_log2e;
+    qreg[4 * s4 + 2] = v.z * a.scale_log2e;
+    qreg[4 * s4 + 3] = v.w * a.scale_log2e;
   }
 }
 
 // Runs key tiles [kt0, kt1) for q tile qt of kv head kvh; writes o rows
-// (normalised) when `final`, else the partial of `slot`.
-template <int D>
+// (normalised) when `final`, else the partial of `slot`. qreg, pk and pv are
+// the caller's so that one q tile can prefetch for the next: with nxt_qt >= 0
+// the first key tile of q tile nxt_qt (key tile 0) is requested into pk/pv
+// during the last key tile, and its q rows into qreg after the loop (their
+// latency then overlaps the combine); the next call passes preloaded = true.
+template <int D, int NPF = kBK * D / 4 / kPThreads>
 __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, float* v_lds,
                                           uint32_t kvh, uint32_t qt, uint32_t kt0, uint32_t kt1,
-                                          bool final, size_t slot) {
+                                          bool final, size_t slot, float (&qreg)[D / 4],
+                                          float4 (&pk)[NPF], float4 (&pv)[NPF], bool preloaded,
+                                          int nxt_qt) {
   constexpr int LDK = D + 4;        // padded K row in LDS (floats)
   constexpr int DS = D / 4;         // k-steps of 4 dims for S
   constexpr int CB = D / 16;        // channel blocks of O^T
-  constexpr int NPF = kBK * D / 4 / kPThreads;
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -160,25 +209,10 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   const bool row_ok = r < a.q_per_tile * a.group && qi < a.n_queries;
   const uint32_t qpos = a.pos0 + qi;
 
-  float4 pk[NPF], pv[NPF];
-  load_tile<D>(pk, pv, a, kvh, kt0, n_keys_total, tid);
-
-  float qreg[DS];
-  {
-    const float4* src = reinterpret_cast<const float4*>(
-        a.q + ((size_t)(row_ok ? qi : q0) * a.n_heads + (row_ok ? h : kvh * a.group)) * D +
-        DS * lg);
-    // q is pre-multiplied by scale * log2(e), so S^T comes out in base-2 units.
-#pragma unroll
-    for (int s4 = 0; s4 < DS / 4; s4++) {
-      const float4 v = src[s4];
-      qreg[4 * s4 + 0] = v.x * a.scale_log2e;
-      qreg[4 * s4 + 1] = v.y * a.scale_log2e;
-      qreg[4 * s4 + 2] = v.z * a.scale_log2e;
-      qreg[4 * s4 + 3] = v.w * a.scale_log2e;
-    }
+  if (!preloaded) {
+    load_tile<D>(pk, pv, a, kvh, kt0, n_keys_total, tid);
+    load_q<D>(qreg, a, kvh, qt);
   }
-
   floatx4 oacc[CB];
 #pragma unroll
   for (int c = 0; c < CB; c++) oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -246,10 +280,22 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
       // Halfway through S (the MFMAs queued so far cover the writes), tile
       // kt + 1 goes from registers into the other buffer and tile kt + 2 is
       // requested (the last one is simply loaded again at the end).
-      if (g == NG / 2 && kt + 1 < kt1) {
-        store_tile<D>(pk, pv, k_lds + (buf ^ 1) * (kBK * LDK), v_lds + (buf ^ 1) * (kBK * D), tid);
-        load_tile<D>(pk, pv, a, kvh, kt + 2 < kt1 ? kt + 2 : kt + 1, n_keys_total, tid);
+      // The next tile goes from registers into the free buffers in two
+      // halves, K a quarter of the way through S and V three quarters of the
+      // way (the MFMAs queued so far cover the writes); the tile after it is
+      // requested right after each half (the last one is simply loaded again
+      // at the end).
+      if (g == NG / 4 && kt + 1 < kt1) {
+        store_k<D>(pk, k_lds + (buf ^ 1) * (kBK * LDK), tid);
+        load_rows<D>(pk, a.kcache, a, kvh, kt + 2 < kt1 ? kt + 2 : kt + 1, n_keys_total, tid);
       }
+      if (g == 3 * NG / 4 && kt + 1 < kt1) {
+        store_v<D>(pv, v_lds + (buf ^ 1) * (kBK * D), tid);
+        load_rows<D>(pv, a.vcache, a, kvh, kt + 2 < kt1 ? kt + 2 : kt + 1, n_keys_total, tid);
+      }
+      // During the last tile, the next q tile's first key tile is requested.
+      if (g == NG / 2 && kt + 1 == kt1 && nxt_qt >= 0)
+        load_tile<D>(pk, pv, a, kvh, 0, n_keys_total, tid);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < 4; j++)
@@ -331,6 +377,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     __syncthreads();  // tile kt + 1 stored; buffer of tile kt free again
   }
 
+  if (nxt_qt >= 0) load_q<D>(qreg, a, kvh, (uint32_t)nxt_qt);  // the next q tile's rows
   l_run = sum_xor<16>(l_run);  // the row's denominator: its four lane groups
   l_run = sum_xor<32>(l_run);
   // ---- combine the two key halves of each row through LDS --------------------
@@ -391,13 +438,17 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
   __shared__ __attribute__((aligned(16))) float v_lds[2 * kBK * D];
   const uint32_t kvh = blockIdx.x % a.n_kv_heads;
   const uint32_t w = blockIdx.x / a.n_kv_heads;
+  constexpr int NPF = kBK * D / 4 / kPThreads;
+  float qreg[D / 4];
+  float4 pk[NPF], pv[NPF];
   if (a.paired) {
     const uint32_t qt_hi = a.n_qtiles - 1 - w;
     run_qtile<D>(a, k_lds, v_lds, kvh, qt_hi, 0,
-                 qtile_kt(qt_hi, a.q_per_tile, a.n_queries, a.pos0), true, 0);
+                 qtile_kt(qt_hi, a.q_per_tile, a.n_queries, a.pos0), true, 0, qreg, pk, pv, false,
+                 w < qt_hi ? (int)w : -1);
     if (w < qt_hi)
       run_qtile<D>(a, k_lds, v_lds, kvh, w, 0, qtile_kt(w, a.q_per_tile, a.n_queries, a.pos0),
-                   true, 0);
+                   true, 0, qreg, pk, pv, true, -1);
     return;
   }
   const uint32_t qt = a.n_qtiles - 1 - w / a.max_splits;  // heaviest q tile first
@@ -408,7 +459,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
   const uint32_t kt0 = split * n_kt / ns;
   const uint32_t kt1 = (split + 1) * n_kt / ns;
   const size_t slot = ((size_t)qt * a.max_splits + split) * a.n_kv_heads + kvh;
-  run_qtile<D>(a, k_lds, v_lds, kvh, qt, kt0, kt1, ns == 1, slot);
+  run_qtile<D>(a, k_lds, v_lds, kvh, qt, kt0, kt1, ns == 1, slot, qreg, pk, pv, false, -1);
 }
 
 // One workgroup per (kv head, q tile, 256 / (D/4) rows); D/4 lanes per row,
