@@ -17,8 +17,9 @@ of the hot path over one batch of synthetic, HBM-resident input:
              ragged decode attention in one call. value in GB/s.
   chunk32k   A 64-token chunk at position 32768 onto a 32768-key cache, 28
              layers: prologue + chunked prefill attention. value in TFLOP/s.
-  decode512  One layer, 513 keys (4.2 MB, fits in the 256 MB MALL, so the
-             figure is an "effective" GB/s).
+  decode512  The same 28-layer step at 513 keys (4.2 MB per layer: it fits in
+             the 256 MB MALL, so the figure is an "effective" GB/s), the 28
+             calls replayed from one captured HIP graph (launch-bound).
   copy       1 GiB device-to-device copy (torch): the reference kernel of
              known traffic that calibrates the FETCH_SIZE / WRITE_SIZE
              counters in profiles/.
@@ -119,6 +120,7 @@ class Workload:
     unit = "GB/s"
     bound = "hbm"
     calls_per_step = 1
+    graph_step = False  # step() replays a captured graph: call time = step time / calls
     data = ("synthetic: seeded N(0,1) q/k/v and K/V caches, norm gains N(1,0.1); no weights "
             "(attention path only)")
 
@@ -244,9 +246,10 @@ class Decode32k(Workload):
             self.call(l)
 
     def config(self):
+        how = ", the layers' calls replayed from one captured HIP graph" if self.graph_step else ""
         return {"workload": f"GQA decode, {self.L} layers x {self.nk} keys (new token at position "
                             f"{self.pos}), per layer fused q/k RMSNorm + RoPE + K/V append + "
-                            "split-K attention",
+                            f"split-K attention{how}",
                 "layers": self.L, "n_keys": self.nk, "n_heads": H, "n_kv_heads": HKV,
                 "head_dim": D, "batch": 1, "kv_cache_bytes": 2 * self.L * self.maxk * HKV * D * 4}
 
@@ -275,10 +278,28 @@ class Decode32k(Workload):
 
 
 class Decode512(Decode32k):
+    """The same layer call at 513 keys (4.2 MB per layer: it fits in the 256 MB
+    MALL, so the figure is an effective GB/s). A call costs about as much as
+    its launches here, so the step -- one call per layer of 28 -- is captured
+    once into a HIP graph and replayed, as a host decoding many tokens would
+    (Model.replay); the call time is the step time / 28."""
+
     name = "decode512"
+    kernel = ("flk_decode_layer x 28 replayed from one HIP graph: decode_split_kernel<128,2,8> + "
+              "decode_merge_kernel<128> per call")
+    graph_step = True
 
     def __init__(self, torch, ops):
-        super().__init__(torch, ops, layers=1, n_keys=513)
+        super().__init__(torch, ops, layers=28, n_keys=513)
+        self.graph = None
+
+    def step(self):
+        if self.graph is None:
+            with self.ops.Graph() as g:
+                for l in range(self.L):
+                    self.call(l)
+            self.graph = g
+        self.graph.launch()
 
 
 class Prefill2k(Workload):
@@ -924,6 +945,8 @@ def measure(torch, stream, w, steps, warmup, calls=None):
     torch.cuda.synchronize()
     wall_ms = (time.perf_counter() - t0) * 1e3 / steps
     ms = start.elapsed_time(end) / steps
+    if w.graph_step:  # the calls are only launched inside the graph
+        return ms, wall_ms, ms / w.calls_per_step
     # Dominant call: R back-to-back calls between two events.
     calls = calls or max(steps * w.calls_per_step, 20)
     torch.cuda.synchronize()
@@ -951,12 +974,16 @@ def run(torch, ops, stream, name, steps, warmup):
     if hasattr(w, "extra"):
         out.update(w.extra(ms, call_ms))
     # Drop the device buffers; the CPU baseline needs only the sizes.
+    if getattr(w, "graph", None) is not None:
+        w.graph.free()
+        w.graph = None
     if hasattr(w, "model"):
         w.model.free()
     for k in [k for k, v in vars(w).items()
               if isinstance(v, (torch.Tensor, list, ops.Workspace, ops.DeviceBuffer, ops.Q8Matrix))
               or k == "model"]:
         delattr(w, k)
+    ops.sync()  # also releases the dropped buffers
     torch.cuda.empty_cache()
     return out, w.cpu_baseline
 

@@ -359,15 +359,18 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs
   }
 
   // Two register sets: the next block's loads are issued before the current
-  // block's arithmetic. Loads are unconditional (a block past the end re-reads
-  // the current one, which is in cache) so the compiler can count them.
+  // block's arithmetic. Loads are unconditional, so the compiler can count
+  // them: past the split's last block a slot loads block 0 instead, which
+  // the tails of all splits request, so after the first request on an XCD it
+  // comes from L2 (the split's own last block, read with the non-temporal
+  // hint, need not still be there); those rows are never used.
   for (uint32_t b = split; b < n_blocks; b += 2 * n_splits) {
     const uint32_t b1 = b + n_splits;
     const uint32_t b2 = b1 + n_splits;
-    load_keys<U, PH>(kn, vn, kb, vb, row4, (b1 < n_blocks ? b1 : b) * KPI, ph, t1);
+    load_keys<U, PH>(kn, vn, kb, vb, row4, (b1 < n_blocks ? b1 : 0) * KPI, ph, t1);
     attend_keys<D, G, U, PH>(ka, va, qv, m, l, acc, b * KPI, ph, t1, owns_pos, pos, knew, vnew,
                              a.scale);
-    load_keys<U, PH>(ka, va, kb, vb, row4, (b2 < n_blocks ? b2 : b) * KPI, ph, t1);
+    load_keys<U, PH>(ka, va, kb, vb, row4, (b2 < n_blocks ? b2 : 0) * KPI, ph, t1);
     if (b1 < n_blocks)
       attend_keys<D, G, U, PH>(kn, vn, qv, m, l, acc, b1 * KPI, ph, t1, owns_pos, pos, knew,
                                vnew, a.scale);
