@@ -464,7 +464,11 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
 
 // One workgroup per (kv head, q tile, 256 / (D/4) rows); D/4 lanes per row,
 // each owning a float4 of channels. Combines the splits of a multi-split q
-// tile with log-sum-exp weights; single-split tiles exit.
+// tile with log-sum-exp weights in one pass: the splits go in rounds of
+// kPMergeBatch whose loads are all issued first (indices past the last split
+// reload it and get weight 0, so every load is unconditional), then folded
+// against a running maximum. Single-split tiles exit.
+constexpr int kPMergeBatch = 8;
 template <int D>
 __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   constexpr int LPR = D / 4;
@@ -479,24 +483,40 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
   const uint32_t qi = qt * a.q_per_tile + r / a.group;
   if (r >= a.q_per_tile * a.group || qi >= a.n_queries) return;
   const uint32_t h = kvh * a.group + r % a.group;
-  float M = -INFINITY;
-  for (uint32_t s = 0; s < ns; s++) {
-    const size_t slot = ((size_t)qt * a.max_splits + s) * a.n_kv_heads + kvh;
-    M = fmaxf(M, a.part_ml[slot * kRows + r].x);
-  }
-  float L = 0.f;
+  float M = -INFINITY, L = 0.f;
   float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-  for (uint32_t s = 0; s < ns; s++) {
-    const size_t slot = ((size_t)qt * a.max_splits + s) * a.n_kv_heads + kvh;
-    const float2 ml = a.part_ml[slot * kRows + r];
-    if (ml.x == -INFINITY) continue;
-    const float w = __builtin_amdgcn_exp2f(ml.x - M);  // m is in log2 units
-    const float4 p = reinterpret_cast<const float4*>(a.part_acc + (slot * kRows + r) * D)[c];
-    L = fmaf(ml.y, w, L);
-    A.x = fmaf(p.x, w, A.x);
-    A.y = fmaf(p.y, w, A.y);
-    A.z = fmaf(p.z, w, A.z);
-    A.w = fmaf(p.w, w, A.w);
+  for (uint32_t s0 = 0; s0 < ns; s0 += kPMergeBatch) {
+    float2 ml[kPMergeBatch];
+    float4 pa[kPMergeBatch];
+#pragma unroll
+    for (int i = 0; i < kPMergeBatch; i++) {
+      const uint32_t sp = min(s0 + i, ns - 1);
+      const size_t slot = ((size_t)qt * a.max_splits + sp) * a.n_kv_heads + kvh;
+      ml[i] = a.part_ml[slot * kRows + r];
+      pa[i] = reinterpret_cast<const float4*>(a.part_acc + (slot * kRows + r) * D)[c];
+    }
+#pragma unroll
+    for (int i = 0; i < kPMergeBatch; i++)
+      if (s0 + i >= ns) ml[i].x = -INFINITY;  // a reloaded split: weight 0
+    float mx = M;
+#pragma unroll
+    for (int i = 0; i < kPMergeBatch; i++) mx = fmaxf(mx, ml[i].x);  // finite: split s0 is live
+    const float wo = __builtin_amdgcn_exp2f(M - mx);  // m is in log2 units; exp2(-inf) = 0
+    L *= wo;
+    A.x *= wo;
+    A.y *= wo;
+    A.z *= wo;
+    A.w *= wo;
+#pragma unroll
+    for (int i = 0; i < kPMergeBatch; i++) {
+      const float w = __builtin_amdgcn_exp2f(ml[i].x - mx);
+      L = fmaf(ml[i].y, w, L);
+      A.x = fmaf(pa[i].x, w, A.x);
+      A.y = fmaf(pa[i].y, w, A.y);
+      A.z = fmaf(pa[i].z, w, A.z);
+      A.w = fmaf(pa[i].w, w, A.w);
+    }
+    M = mx;
   }
   float4* dst = reinterpret_cast<float4*>(a.o + ((size_t)qi * a.n_heads + h) * D);
   dst[c] = make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
