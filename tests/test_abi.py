@@ -36,15 +36,43 @@ def test_every_header_is_listed():
         f for f in os.listdir(os.path.join(ROOT, "include")) if f.endswith(".h"))
 
 
+def declared_arity() -> dict[str, int]:
+    """Entry point -> parameter count of its prototype in include/*.h."""
+    out = {}
+    for h in HEADERS:
+        text = re.sub(r"/\*.*?\*/", "", open(h).read(), flags=re.S)
+        for name, params in re.findall(r"\b(flk_\w+)\s*\(([^;{]*?)\)\s*;", text, flags=re.S):
+            params = params.strip()
+            out[name] = 0 if params in ("", "void") else params.count(",") + 1
+    return out
+
+
 def test_header_and_binding_agree():
     assert declared_functions() == set(_lib.SIGNATURES)
+    arity = declared_arity()
+    assert set(arity) == declared_functions()
+    for name, (_, args) in _lib.SIGNATURES.items():
+        assert len(args) == arity[name], (name, len(args), arity[name])
 
 
-def test_integration_binding_lists_every_declared_symbol():
-    """INTEGRATION.md's Deno.dlopen table names every entry point, no more."""
-    text = open(os.path.join(ROOT, "INTEGRATION.md")).read()
-    bound = set(re.findall(r"\b(flk_\w+):\s*\{\s*parameters", text))
-    assert bound == declared_functions(), (declared_functions() - bound, bound - declared_functions())
+def deno_binding() -> dict[str, int]:
+    """Entry point -> parameter count of the Deno.dlopen table in
+    flock_amd/deno/hip_attn.ts (the TypeScript host's binding)."""
+    text = open(os.path.join(ROOT, "flock_amd", "deno", "hip_attn.ts")).read()
+    table = {}
+    for name, params in re.findall(r"\b(flk_\w+):\s*\{\s*parameters:\s*\[(.*?)\]", text, flags=re.S):
+        table[name] = len([p for p in params.split(",") if p.strip()])
+    return table
+
+
+def test_deno_binding_lists_every_declared_symbol_with_its_arity():
+    """The Deno binding binds every entry point, no more, each with as many
+    parameters as its C prototype (and the ctypes table) has."""
+    table = deno_binding()
+    assert set(table) == declared_functions(), (declared_functions() - set(table),
+                                                set(table) - declared_functions())
+    for name, n in table.items():
+        assert n == len(_lib.SIGNATURES[name][1]), (name, n, len(_lib.SIGNATURES[name][1]))
 
 
 def test_library_exports_every_declared_symbol():

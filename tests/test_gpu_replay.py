@@ -57,8 +57,13 @@ def replay_chunks(frames: list[bytes], hidden: int):
     Yields (offset, n_tokens, activations)."""
     for off in range(0, len(frames), REPLAY_CHUNK):
         chunk = frames[off:off + REPLAY_CHUNK]
+        want_flags = FLAG_REPLAY | (FLAG_RESET if off == 0 else 0)
         payload = bytearray()
-        for i, f in enumerate(chunk):
+        for i, journaled in enumerate(chunk):
+            head = ctypes.create_string_buffer(20)  # re-sent with the replay flags
+            ops.check(_lib.lib().flk_wire_header_pack(off + i, hidden, off + i, want_flags, head),
+                      "header")
+            f = head.raw + journaled[20:]
             seq, hid, offset, flags, nvals = (ctypes.c_uint32(), ctypes.c_uint32(),
                                               ctypes.c_uint32(), ctypes.c_uint32(),
                                               ctypes.c_uint64())
@@ -66,6 +71,7 @@ def replay_chunks(frames: list[bytes], hidden: int):
                 f, len(f), ctypes.byref(seq), ctypes.byref(hid), ctypes.byref(offset),
                 ctypes.byref(flags), ctypes.byref(nvals)), "unpack")
             assert hid.value == hidden and offset.value == off + i and nvals.value == hidden
+            assert flags.value == want_flags
             payload += f[20:]
         h16 = ops.DeviceBuffer.from_array(np.frombuffer(bytes(payload), "<u2"))
         out = ops.DeviceBuffer(4 * len(chunk) * hidden)
