@@ -313,6 +313,10 @@ int32_t flk_attn_prefill(const float* q, const float* kcache, const float* vcach
   if (n_queries == 0) return fail(FLK_ERR_ARG, "prefill n_queries must be >= 1");
   if ((uint64_t)pos0 + n_queries > 0xFFFFFFFFull)
     return fail(FLK_ERR_ARG, "pos0 + n_queries overflows");
+  // The kernel addresses a 64-row key tile with 32-bit byte offsets.
+  if ((uint64_t)n_kv_heads * head_dim * 4 * 64 > 0x7FFFFFFFull)
+    return fail(FLK_ERR_UNSUPPORTED, "prefill: %u kv heads x %u dims exceed a 64-row tile's 2 GiB",
+                n_kv_heads, head_dim);
   const PrefillPlan p = prefill_plan(n_heads, n_kv_heads, head_dim, n_queries, pos0);
   rc = check_ws(ws, ws_bytes, prefill_ws_bytes(p, head_dim));
   if (rc) return rc;

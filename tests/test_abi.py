@@ -254,3 +254,12 @@ def test_noalloc_decode_rejects_calls_beyond_its_static_scratch():
     rc, msg = code_and_msg(L.flk_decode_layer_noalloc(*([FAKE] * 6), 1e-6, 0, *([FAKE] * 4),
                                                       2048, 16, 8, 128, 2048))
     assert rc == _lib.FLK_ERR_CACHE_FULL
+
+
+def test_prefill_rejects_rows_too_wide_for_its_tile_offsets():
+    # A 64-row key tile is addressed with 32-bit byte offsets: 65536 kv heads
+    # of 128 floats make a tile of 2 GiB, which is refused on the host.
+    L = _lib.lib()
+    rc, msg = code_and_msg(L.flk_attn_prefill(FAKE, FAKE, FAKE, FAKE, 65536, 65536, 128, 4, 0,
+                                              FAKE, 1 << 40))
+    assert rc == _lib.FLK_ERR_UNSUPPORTED and "2 GiB" in msg
