@@ -29,9 +29,15 @@ namespace flk {
 
 constexpr int kQ8Lanes = 64;      // the reference's LANES (q8_coop.wgsl:58)
 constexpr int kQ8Threads = 256;   // 4 waves
-// Row groups whose loads are in flight together (fewer when x takes more registers).
+// Row groups whose loads are in flight together (fewer when x takes more
+// registers). 151936 x 1024 (the LM head): 32.3 us with 4, 30.7 with 2, 30.6
+// with 1, 32.5 with 3; a second register set requesting the next groups before
+// the current ones are folded, 32.3 (2 + 2) to 34.1 (4 + 4); the weights read
+// with the non-temporal hint, 32.2. A greedy token at 513 keys (graph replay):
+// 0.999 ms with 4 everywhere, 0.982 with 2, 0.969 with 2 here and 4 where an
+// input fusion is compiled in (FLK_Q8_UNROLL_FUSED).
 #ifndef FLK_Q8_UNROLL
-#define FLK_Q8_UNROLL 4
+#define FLK_Q8_UNROLL 2
 #endif
 #ifndef FLK_Q8_WG_PER_CU
 #define FLK_Q8_WG_PER_CU 0  // 0: as many as fit (occupancy query)
@@ -48,8 +54,15 @@ constexpr int kQ8Threads = 256;   // 4 waves
 #ifndef FLK_Q8_MM_WAVES1
 #define FLK_Q8_MM_WAVES1 3  // rows of at most 1024 columns
 #endif
-template <int NB>
-constexpr int q8_unroll() { return NB == 1 ? FLK_Q8_UNROLL : (NB == 2 ? 2 : 1); }
+// With an input fusion every wave recomputes the fused input's norm, so fewer
+// waves (more row groups each) pay it fewer times.
+#ifndef FLK_Q8_UNROLL_FUSED
+#define FLK_Q8_UNROLL_FUSED 4
+#endif
+template <int NB, bool FUSE>
+constexpr int q8_unroll() {
+  return NB == 1 ? (FUSE ? FLK_Q8_UNROLL_FUSED : FLK_Q8_UNROLL) : (NB == 2 ? 2 : 1);
+}
 constexpr int kQ8MaxRegBlocks = 4;  // x blocks per lane kept in registers (8192 columns)
 #ifndef FLK_Q8_LDS_TREE_ROWS
 #define FLK_Q8_LDS_TREE_ROWS 65536
@@ -219,7 +232,7 @@ __device__ __forceinline__ void q8_load_rows(const Q8Args& a, uint32_t g0, uint3
 template <int P, int NB, bool FUSE, bool LDS_TREE = false>
 __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
   constexpr int R = kWave / P;  // rows per wave per step
-  constexpr int kQ8Unroll = q8_unroll<NB>();
+  constexpr int kQ8Unroll = q8_unroll<NB, FUSE>();
   const int lane = threadIdx.x & 63;
   const int ll = lane % P;      // logical lane
   const int sub = lane / P;     // which row of the group
@@ -726,7 +739,7 @@ static uint32_t q8_grid_x(uint32_t n_groups) {
       cus_of[dev] = 256;
     cus = cus_of[dev];
   }
-  const uint32_t per_wg = (kQ8Threads / kWave) * q8_unroll<NB>();
+  const uint32_t per_wg = (kQ8Threads / kWave) * q8_unroll<NB, FUSE>();
   const uint32_t need = (n_groups + per_wg - 1) / per_wg;
   const uint32_t cap = (uint32_t)(per_cu * cus);
   return need < cap ? (need > 0 ? need : 1) : cap;
