@@ -133,13 +133,17 @@ __device__ __forceinline__ void q8_fused_block(const Q8Args& a, const float* xt,
 // tree's stride-64 step, and the xor butterfly over the wave is its strides
 // 32 .. 1; scale = 1 / sqrt(mean + eps) rounded once. (A workgroup barrier
 // would also wait for the weight loads already in flight.)
+#ifndef FLK_Q8_NORM_BATCH
+#define FLK_Q8_NORM_BATCH 16
+#endif
 template <class LOAD>
 __device__ __forceinline__ float q8_rms_scale(uint32_t n, float eps, LOAD ld) {
   const uint32_t l = threadIdx.x & 63;
-  // Elements l + 64k: even k feed partial l, odd k partial l + 64. Eight are
-  // loaded before any is used (a load-use loop would serialise the
-  // latencies); past the end they read 0, which adds exactly nothing.
-  constexpr int kB = 8;
+  // Elements l + 64k: even k feed partial l, odd k partial l + 64. A batch of
+  // kB is loaded before any is used (a load-use loop would serialise the
+  // latencies; 16 cover a 1024-wide row in one round trip); past the end
+  // they read 0, which adds exactly nothing.
+  constexpr int kB = FLK_Q8_NORM_BATCH;
   float p0 = 0.f, p1 = 0.f;
   for (uint32_t base = l; base < n; base += 64 * kB) {
     float v[kB];
