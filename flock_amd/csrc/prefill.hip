@@ -277,9 +277,6 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
         for (int b = 0; b < kHalfKB; b++) kg[(g + kAhead) % (kAhead + 1)][b] = k_group(kb, g + kAhead, b);
       }
       __builtin_amdgcn_sched_barrier(0);
-      // Halfway through S (the MFMAs queued so far cover the writes), tile
-      // kt + 1 goes from registers into the other buffer and tile kt + 2 is
-      // requested (the last one is simply loaded again at the end).
       // The next tile goes from registers into the free buffers in two
       // halves, K a quarter of the way through S and V three quarters of the
       // way (the MFMAs queued so far cover the writes); the tile after it is
@@ -384,8 +381,9 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   // Lane holds channels 4*CB*lg + CB*j + c of its row. The upper waves park
   // their (m, l, acc) in the (now free) K tile buffer; the lower waves fold
   // them in and write the row.
-  float* m_lds = k_lds;  // every wave passed the last tile's barrier                 // [kRows] m, then [kRows] l
-  float* o_lds = k_lds + 2 * kRows;     // [kRows][D]
+  // Every wave has passed the last tile's barrier, so the K buffers are free.
+  float* m_lds = k_lds;              // [kRows] m, then [kRows] l
+  float* o_lds = k_lds + 2 * kRows;  // [kRows][D]
   if (half == 1) {
     float* dst = o_lds + r * D + 4 * CB * lg;
 #pragma unroll
