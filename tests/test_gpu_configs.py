@@ -175,7 +175,7 @@ def test_ragged_batch_of_64(rng):
     got = o.download(B * H * D).reshape(B, H * D)
     oracle.set_threads(min(16, os.cpu_count() or 1))
     row = HKV * D
-    worst, ties = None, 0
+    worst, ties, ids_equal = None, 0, 0
     for b in range(B):
         s, n = int(offs[b]) * row, int(lens[b])
         qb = q[b * H * D:(b + 1) * H * D]
@@ -185,7 +185,9 @@ def test_ragged_batch_of_64(rng):
         assert meets_bar(m), (b, n, fmt(m))
         ids = check_ids(f"ragged sequence {b}", got[b], want, H, m["max_abs"])
         ties += ids["near_tie_rows"]
+        ids_equal += int(ids["projection_id_equal"])
         if worst is None or m["rel"] > worst[1]["rel"]:
             worst = (b, m)
     record("ragged decode, 64 sequences (worst of 64)", worst[1], seq=worst[0],
-           n_keys=int(lens[worst[0]]), sum_n_keys=rows, rows=B * H, near_tie_rows=ties)
+           n_keys=int(lens[worst[0]]), sum_n_keys=rows, rows=B * H, near_tie_rows=ties,
+           projection_ids_equal=ids_equal, sequences=B)
