@@ -1,0 +1,109 @@
+"""Closed-form properties at the benchmark sizes, on the GPU, without the oracle.
+
+Two inputs make attention's answer known exactly:
+
+- every key row of a kv head equal: all scores of a query are equal, every
+  softmax weight is exp(0) = 1, and the output is the plain mean of the V
+  rows the query sees (for causal prefill, query i at position p sees rows
+  0..p: a prefix mean). Computed here in float64 with cumulative sums. A key
+  block dropped, counted twice or masked wrongly moves a 32769-row mean by
+  ~1e-5 (one 4-key block of N(0,1) rows); rounding moves it by ~1e-9.
+- every V row of a kv head equal to c: whatever the weights, the output is c.
+  This pins the softmax normalisation through the split-K merge (an
+  accumulator and a denominator rescaled differently show up at once).
+
+The sizes are the benchmark configurations': decode over 32769 keys, causal
+prefill of 2048 tokens, and a 64-token chunk onto 32768 cached keys (key
+splits + merge).
+"""
+from __future__ import annotations
+
+import numpy as np
+import pytest
+
+from conftest import randn
+
+pytestmark = pytest.mark.gpu
+
+from flock_amd import ops  # noqa: E402  (no skip: a missing library must fail)
+
+H, HKV, D = 16, 8, 128
+G = H // HKV
+
+
+def dev(a) -> "ops.DeviceBuffer":
+    return ops.DeviceBuffer.from_array(np.ascontiguousarray(a, np.float32))
+
+
+def equal_keys(rng, n_keys: int) -> np.ndarray:
+    """[n_keys][HKV][D] with every row of a kv head the same random vector."""
+    row = randn(rng, HKV * D).reshape(1, HKV, D)
+    return np.ascontiguousarray(np.broadcast_to(row, (n_keys, HKV, D))).ravel()
+
+
+def prefix_means(v: np.ndarray, n_keys: int) -> np.ndarray:
+    """[n_keys][HKV][D] float64: row t holds the mean of V rows 0..t."""
+    c = np.cumsum(v.reshape(n_keys, HKV, D).astype(np.float64), axis=0)
+    return c / np.arange(1, n_keys + 1, dtype=np.float64)[:, None, None]
+
+
+def test_decode_equal_keys_give_the_mean_of_v(rng):
+    nk = 32769
+    k, v = equal_keys(rng, nk), randn(rng, nk * HKV * D)
+    q = randn(rng, H * D)
+    o = ops.DeviceBuffer(H * D * 4)
+    ops.attn_decode(dev(q), dev(k), dev(v), o, H, HKV, D, nk, ops.Workspace(H, HKV, D, nk))
+    ops.sync()
+    got = o.download(H * D).reshape(H, D)
+    mean = v.reshape(nk, HKV, D).astype(np.float64).mean(axis=0)  # [HKV][D]
+    want = np.repeat(mean, G, axis=0)                               # head h reads kv head h // G
+    err = float(np.max(np.abs(got - want)))
+    assert err < 1e-7, err
+
+
+def test_decode_uniform_v_is_returned(rng):
+    nk = 32769
+    k = randn(rng, nk * HKV * D)
+    c = randn(rng, HKV * D).reshape(1, HKV, D)
+    v = np.ascontiguousarray(np.broadcast_to(c, (nk, HKV, D))).ravel()
+    q = randn(rng, H * D)
+    o = ops.DeviceBuffer(H * D * 4)
+    ops.attn_decode(dev(q), dev(k), dev(v), o, H, HKV, D, nk, ops.Workspace(H, HKV, D, nk))
+    ops.sync()
+    got = o.download(H * D).reshape(H, D)
+    want = np.repeat(c[0].astype(np.float64), G, axis=0)
+    rel = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+    assert rel < 1e-5, rel
+
+
+@pytest.mark.parametrize("n,pos0", [(2048, 0), (64, 32768)])
+def test_prefill_equal_keys_give_causal_prefix_means(rng, n, pos0):
+    nk = pos0 + n
+    k, v = equal_keys(rng, nk), randn(rng, nk * HKV * D)
+    q = randn(rng, n * H * D)
+    o = ops.DeviceBuffer(n * H * D * 4)
+    ops.attn_prefill(dev(q), dev(k), dev(v), o, H, HKV, D, n, pos0,
+                     ops.Workspace(H, HKV, D, nk, n))
+    ops.sync()
+    got = o.download(n * H * D).reshape(n, H, D)
+    means = prefix_means(v, nk)[pos0:pos0 + n]                      # query i sees rows 0..pos0+i
+    want = np.repeat(means, G, axis=1)
+    err = float(np.max(np.abs(got - want)))
+    assert err < 2e-7, err
+
+
+@pytest.mark.parametrize("n,pos0", [(2048, 0), (64, 32768)])
+def test_prefill_uniform_v_is_returned(rng, n, pos0):
+    nk = pos0 + n
+    k = randn(rng, nk * HKV * D)
+    c = randn(rng, HKV * D).reshape(1, HKV, D)
+    v = np.ascontiguousarray(np.broadcast_to(c, (nk, HKV, D))).ravel()
+    q = randn(rng, n * H * D)
+    o = ops.DeviceBuffer(n * H * D * 4)
+    ops.attn_prefill(dev(q), dev(k), dev(v), o, H, HKV, D, n, pos0,
+                     ops.Workspace(H, HKV, D, nk, n))
+    ops.sync()
+    got = o.download(n * H * D).reshape(n, H, D)
+    want = np.broadcast_to(np.repeat(c[0].astype(np.float64), G, axis=0), (n, H, D))
+    rel = float(np.max(np.abs(got - want)) / np.max(np.abs(want)))
+    assert rel < 1e-5, rel
