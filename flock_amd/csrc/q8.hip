@@ -59,6 +59,18 @@ constexpr int kQ8Threads = 256;   // 4 waves
 #ifndef FLK_Q8_UNROLL_FUSED
 #define FLK_Q8_UNROLL_FUSED 4
 #endif
+// Request order (0 for the older orders, kept for A/B builds). A greedy token
+// at 513 keys, graph replay, ms per 32 tokens: residuals read after each
+// row's sum and the norm's loads after the weights 30.98-31.00; residuals
+// requested with the weights 30.22-30.26; and the norm's first batch ahead of
+// the weights 29.40-29.51; the fused x and gain also requested before the
+// norm's reduction (one round trip fewer, 32 more registers) 29.65.
+#ifndef FLK_Q8_RES_EARLY
+#define FLK_Q8_RES_EARLY 1
+#endif
+#ifndef FLK_Q8_NORM_FIRST
+#define FLK_Q8_NORM_FIRST 1
+#endif
 template <int NB, bool FUSE>
 constexpr int q8_unroll() {
   return NB == 1 ? (FUSE ? FLK_Q8_UNROLL_FUSED : FLK_Q8_UNROLL) : (NB == 2 ? 2 : 1);
@@ -94,18 +106,23 @@ __device__ __forceinline__ float q8_swiglu(float g, float u) {
   return (g / (1.f + e)) * u;
 }
 
-// Fused inputs c0 .. c0 + 31 of one token (xt: the token's x, tok_off: its
-// offset in x and up).
-__device__ __forceinline__ void q8_fused_block(const Q8Args& a, const float* xt, size_t tok_off,
-                                               uint32_t c0, float scale, float (&out)[32]) {
-  float4 xv[8], yv[8];
+// Loads of fused inputs c0 .. c0 + 31 of one token (xt: the token's x,
+// tok_off: its offset in x and up): x, and the norm gain or the up values.
+__device__ __forceinline__ void q8_fused_load(const Q8Args& a, const float* xt, size_t tok_off,
+                                              uint32_t c0, float4 (&xv)[8], float4 (&yv)[8]) {
   const float4* xs = reinterpret_cast<const float4*>(xt + c0);
+  const float4* ys = reinterpret_cast<const float4*>(
+      a.norm_gain != nullptr ? a.norm_gain + c0 : a.up + tok_off + c0);
 #pragma unroll
   for (int i = 0; i < 8; i++) xv[i] = xs[i];
-  if (a.norm_gain != nullptr) {  // uniform
-    const float4* gs = reinterpret_cast<const float4*>(a.norm_gain + c0);
 #pragma unroll
-    for (int i = 0; i < 8; i++) yv[i] = gs[i];
+  for (int i = 0; i < 8; i++) yv[i] = ys[i];
+}
+
+// The fused inputs from those loads (scale: the token's rmsnorm scale).
+__device__ __forceinline__ void q8_fused_apply(const Q8Args& a, float scale, const float4 (&xv)[8],
+                                               const float4 (&yv)[8], float (&out)[32]) {
+  if (a.norm_gain != nullptr) {  // uniform
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       out[4 * i + 0] = (xv[i].x * scale) * yv[i].x;
@@ -114,9 +131,6 @@ __device__ __forceinline__ void q8_fused_block(const Q8Args& a, const float* xt,
       out[4 * i + 3] = (xv[i].w * scale) * yv[i].w;
     }
   } else {
-    const float4* us = reinterpret_cast<const float4*>(a.up + tok_off + c0);
-#pragma unroll
-    for (int i = 0; i < 8; i++) yv[i] = us[i];
 #pragma unroll
     for (int i = 0; i < 8; i++) {
       out[4 * i + 0] = q8_swiglu(xv[i].x, yv[i].x);
@@ -125,6 +139,14 @@ __device__ __forceinline__ void q8_fused_block(const Q8Args& a, const float* xt,
       out[4 * i + 3] = q8_swiglu(xv[i].w, yv[i].w);
     }
   }
+}
+
+// Both steps (x read straight from memory).
+__device__ __forceinline__ void q8_fused_block(const Q8Args& a, const float* xt, size_t tok_off,
+                                               uint32_t c0, float scale, float (&out)[32]) {
+  float4 xv[8], yv[8];
+  q8_fused_load(a, xt, tok_off, c0, xv, yv);
+  q8_fused_apply(a, scale, xv, yv, out);
 }
 
 // rmsnorm scale of a token's n elements, read through ld(i) from any memory
@@ -136,32 +158,54 @@ __device__ __forceinline__ void q8_fused_block(const Q8Args& a, const float* xt,
 #ifndef FLK_Q8_NORM_BATCH
 #define FLK_Q8_NORM_BATCH 16
 #endif
+constexpr int kQ8NormBatch = FLK_Q8_NORM_BATCH;
+
+// One batch: elements base + 64k, k < kQ8NormBatch (0 past the end).
 template <class LOAD>
-__device__ __forceinline__ float q8_rms_scale(uint32_t n, float eps, LOAD ld) {
+__device__ __forceinline__ void q8_rms_load(uint32_t base, uint32_t n, LOAD ld,
+                                            float (&v)[kQ8NormBatch]) {
+#pragma unroll
+  for (int k = 0; k < kQ8NormBatch; k++) {
+    const uint32_t i = base + 64 * k;
+    v[k] = ld(min(i, n - 1));
+    v[k] = i < n ? v[k] : 0.f;
+  }
+}
+
+__device__ __forceinline__ void q8_rms_fold(const float (&v)[kQ8NormBatch], float& p0, float& p1) {
+#pragma unroll
+  for (int k = 0; k < kQ8NormBatch; k += 2) {
+    p0 = fma32(v[k], v[k], p0);
+    p1 = fma32(v[k + 1], v[k + 1], p1);
+  }
+}
+
+// Batches after the first (elements from 64 * kQ8NormBatch on), folded, then
+// the tree and the scale.
+template <class LOAD>
+__device__ __forceinline__ float q8_rms_rest(float p0, float p1, uint32_t n, float eps, LOAD ld) {
   const uint32_t l = threadIdx.x & 63;
-  // Elements l + 64k: even k feed partial l, odd k partial l + 64. A batch of
-  // kB is loaded before any is used (a load-use loop would serialise the
-  // latencies; 16 cover a 1024-wide row in one round trip); past the end
-  // they read 0, which adds exactly nothing.
-  constexpr int kB = FLK_Q8_NORM_BATCH;
-  float p0 = 0.f, p1 = 0.f;
-  for (uint32_t base = l; base < n; base += 64 * kB) {
-    float v[kB];
-#pragma unroll
-    for (int k = 0; k < kB; k++) {
-      const uint32_t i = base + 64 * k;
-      v[k] = ld(min(i, n - 1));
-      v[k] = i < n ? v[k] : 0.f;
-    }
-#pragma unroll
-    for (int k = 0; k < kB; k += 2) {
-      p0 = fma32(v[k], v[k], p0);
-      p1 = fma32(v[k + 1], v[k + 1], p1);
-    }
+  for (uint32_t base = l + 64 * kQ8NormBatch; base < n; base += 64 * kQ8NormBatch) {
+    float v[kQ8NormBatch];
+    q8_rms_load(base, n, ld, v);
+    q8_rms_fold(v, p0, p1);
   }
   const float sum = tree_sum64(p0 + p1);
   const float mean = sum / (float)n;
   return rsqrt_once(mean + eps);
+}
+
+template <class LOAD>
+__device__ __forceinline__ float q8_rms_scale(uint32_t n, float eps, LOAD ld) {
+  // Elements l + 64k: even k feed partial l, odd k partial l + 64. A batch of
+  // kQ8NormBatch is loaded before any is used (a load-use loop would
+  // serialise the latencies; 16 cover a 1024-wide row in one round trip);
+  // past the end they read 0, which adds exactly nothing.
+  float v[kQ8NormBatch];
+  q8_rms_load(threadIdx.x & 63, n, ld, v);
+  float p0 = 0.f, p1 = 0.f;
+  q8_rms_fold(v, p0, p1);
+  return q8_rms_rest(p0, p1, n, eps, ld);
 }
 
 // The scale of token row xt in global memory; 1 when there is no norm.
@@ -227,6 +271,21 @@ __device__ __forceinline__ void q8_load_rows(const Q8Args& a, uint32_t g0, uint3
   }
 }
 
+// Residuals of the same row groups (o <- res + W x), requested with their
+// weights rather than after the row's sum, which would add a memory round
+// trip to the end of every group. Rows past the end re-read the last row.
+template <int P, int UR>
+__device__ __forceinline__ void q8_load_res(const Q8Args& a, uint32_t tok, uint32_t g0,
+                                            uint32_t waves, int sub, float (&rv)[UR]) {
+  constexpr int R = kWave / P;
+  if (a.res == nullptr) return;  // uniform
+#pragma unroll
+  for (int u = 0; u < UR; u++) {
+    const uint32_t row = min((g0 + waves * u) * R + sub, a.n_rows - 1);
+    rv[u] = a.res[(size_t)tok * a.n_rows + row];
+  }
+}
+
 // P logical lanes per row, NB x blocks per lane in registers (NB * 64 >= the
 // row's block count). Grid: (workgroups over row groups, tokens).
 // FUSE: the input fusions (rmsnorm / swiglu) are compiled in.
@@ -245,17 +304,34 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
   const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
   const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
 
-  // The first row groups' weights are requested before x is prepared, so
-  // the input fusion's latency (the norm's reduction) overlaps their fetch.
+  // The first row groups' weights (and residuals) are requested before x is
+  // prepared, so the input fusion's latency overlaps their fetch.
+  const size_t tok_off = (size_t)tok * a.n_cols;
+  const float* xt = a.x + tok_off;
+  auto ldx = [xt](uint32_t i) { return xt[i]; };
+  // With the norm first, its first batch of x is requested before the
+  // weights: loads return in order, so its sum of squares is formed while
+  // the weights are still on their way.
+  float nv[kQ8NormBatch];
+  if (FUSE && FLK_Q8_NORM_FIRST) q8_rms_load(lane, a.n_cols, ldx, nv);
   uint4 w0[kQ8Unroll][NB], w1[kQ8Unroll][NB];
   uint16_t hs[kQ8Unroll][NB];
+  float rv[kQ8Unroll] = {};
   q8_load_rows<P, NB, kQ8Unroll>(a, wave, waves, ll, sub, nb, w0, w1, hs);
+  if (FLK_Q8_RES_EARLY) q8_load_res<P, kQ8Unroll>(a, tok, wave, waves, sub, rv);
 
   // x blocks ll, ll + 64, ... of this token (zeros past the row's end),
   // after the optional input fusion.
-  const size_t tok_off = (size_t)tok * a.n_cols;
-  const float* xt = a.x + tok_off;
-  const float scale = FUSE ? q8_norm_scale(a, xt) : 1.f;
+  float scale = 1.f;
+  if (FUSE && FLK_Q8_NORM_FIRST) {
+    if (a.norm_gain != nullptr) {  // uniform
+      float p0 = 0.f, p1 = 0.f;
+      q8_rms_fold(nv, p0, p1);
+      scale = q8_rms_rest(p0, p1, a.n_cols, a.norm_eps, ldx);
+    }
+  } else if (FUSE) {
+    scale = q8_norm_scale(a, xt);
+  }
   float xr[NB][32];
   bool live[NB];
 #pragma unroll
@@ -288,7 +364,10 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
   for (uint32_t g0 = wave; g0 < n_groups; g0 += waves * kQ8Unroll) {
     // Loads of kQ8Unroll row groups first, then the arithmetic (the first
     // groups were loaded above).
-    if (g0 != wave) q8_load_rows<P, NB, kQ8Unroll>(a, g0, waves, ll, sub, nb, w0, w1, hs);
+    if (g0 != wave) {
+      q8_load_rows<P, NB, kQ8Unroll>(a, g0, waves, ll, sub, nb, w0, w1, hs);
+      if (FLK_Q8_RES_EARLY) q8_load_res<P, kQ8Unroll>(a, tok, g0, waves, sub, rv);
+    }
 #pragma unroll
     for (int u = 0; u < kQ8Unroll; u++) {
       float part = 0.f;
@@ -311,7 +390,7 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
       }
       if (ll == 0 && g0 + waves * u < n_groups && row < a.n_rows) {
         const size_t oi = (size_t)tok * a.n_rows + row;
-        if (a.res != nullptr) part = a.res[oi] + part;
+        if (a.res != nullptr) part = (FLK_Q8_RES_EARLY ? rv[u] : a.res[oi]) + part;
         if (a.o != nullptr) a.o[oi] = part;
         if (argmax_better(part, row, bv, bi)) {
           bv = part;
