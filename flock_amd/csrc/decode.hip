@@ -90,8 +90,17 @@ constexpr int kMergeCols = 8;    // float4 columns per merge workgroup (32 chann
 constexpr int kMergeBatch = 8;   // splits per thread per round of loads
 
 // Keys per slot per iteration: fewer when G is large, to bound registers.
-__host__ __device__ constexpr int decode_unroll(int G) {
-  return G <= 4 ? FLK_DECODE_UNROLL : (FLK_DECODE_UNROLL > 1 ? FLK_DECODE_UNROLL / 2 : 1);
+// Ragged batches (many shorter-lived workgroups, each paying its first rows'
+// latency) keep more rows in flight: 64 sequences, 1025..16385 keys, 731 ->
+// 712 us per call with 4 instead of 2; one 32769-key sequence is slower
+// with 4 (45.4 -> 47.2 us per fused call).
+#ifndef FLK_DECODE_RAGGED_UNROLL
+#define FLK_DECODE_RAGGED_UNROLL 4
+#endif
+__host__ __device__ constexpr int decode_unroll(int G, bool ragged) {
+  return ragged ? (G <= 4 ? FLK_DECODE_RAGGED_UNROLL
+                          : (FLK_DECODE_RAGGED_UNROLL > 1 ? FLK_DECODE_RAGGED_UNROLL / 2 : 1))
+                : (G <= 4 ? FLK_DECODE_UNROLL : (FLK_DECODE_UNROLL > 1 ? FLK_DECODE_UNROLL / 2 : 1));
 }
 
 // Splits of a sequence with n_keys keys: ceil(blocks / bps), at most
@@ -202,13 +211,13 @@ __device__ __forceinline__ void attend_keys(const float4 (&kr_in)[U], const floa
   }
 }
 
-template <int D, int G, int KH>
+template <int D, int G, int KH, bool RAGGED>
 __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs a) {
   constexpr int LPK = D / 4;                    // lanes per (key, kv head) row
   constexpr int SLOTS = kDecodeThreads / LPK;   // 16 (D = 128) or 32 (D = 64) at 512 threads
   static_assert(SLOTS % KH == 0, "KH must divide the slot count");
   constexpr int PH = SLOTS / KH;                // key phases
-  constexpr int U = decode_unroll(G);
+  constexpr int U = decode_unroll(G, RAGGED);
   constexpr int KPI = PH * U;                   // keys per iteration
   constexpr int HG = KH * G;                    // q heads of this workgroup
 
@@ -537,10 +546,11 @@ static uint32_t kv_heads_per_wg(uint32_t n_kv_heads) {
   return 1;
 }
 
-// Keys per loop iteration of one workgroup (PH * U).
-static uint32_t keys_per_iter(const DecodeShape& s) {
+// Keys per loop iteration of one workgroup (PH * U) for calls of n_seqs
+// sequences (more than one: the ragged instance).
+static uint32_t keys_per_iter(const DecodeShape& s, uint32_t n_seqs) {
   const uint32_t slots = kDecodeThreads / (s.head_dim / 4);
-  const uint32_t U = decode_unroll((int)(s.n_heads / s.n_kv_heads));
+  const uint32_t U = decode_unroll((int)(s.n_heads / s.n_kv_heads), n_seqs > 1);
   return slots / kv_heads_per_wg(s.n_kv_heads) * U;
 }
 
@@ -563,7 +573,7 @@ struct SplitPlan {
 
 static SplitPlan split_plan(const DecodeShape& s) {
   SplitPlan p{};
-  p.kpi = keys_per_iter(s);
+  p.kpi = keys_per_iter(s, s.n_seqs);
   const uint64_t groups = s.n_kv_heads / kv_heads_per_wg(s.n_kv_heads);
   const uint64_t nb = ((uint64_t)s.max_n_keys + p.kpi - 1) / p.kpi;
   if (s.n_seqs == 1) {
@@ -597,12 +607,12 @@ uint64_t decode_ws_bytes(const DecodeShape& s) {
 // max_splits = ceil(nb / bps) <= kRaggedTargetWG / (groups * n) + 1; both
 // also <= ceil(nb / kMinBps). Take the largest n * splits.
 uint64_t decode_ws_bound(const DecodeShape& s) {
-  const uint64_t kpi = keys_per_iter(s);
   const uint64_t groups = s.n_kv_heads / kv_heads_per_wg(s.n_kv_heads);
-  const uint64_t nb = ((uint64_t)s.max_n_keys + kpi - 1) / kpi;
-  const uint64_t by_len = (nb + kMinBps - 1) / kMinBps;
   uint64_t best = 0;
   for (uint64_t n = 1; n <= s.n_seqs; n++) {
+    const uint64_t kpi = keys_per_iter(s, (uint32_t)n);
+    const uint64_t nb = ((uint64_t)s.max_n_keys + kpi - 1) / kpi;
+    const uint64_t by_len = (nb + kMinBps - 1) / kMinBps;
     const uint64_t by_wg = n == 1 ? (kTargetWG / groups > 0 ? kTargetWG / groups : 1)
                                   : kRaggedTargetWG / (groups * n) + 1;
     const uint64_t splits = by_len < by_wg ? by_len : by_wg;
@@ -611,12 +621,13 @@ uint64_t decode_ws_bound(const DecodeShape& s) {
   return best ? ws_for_slots(best * s.n_heads, s.head_dim) : 0;
 }
 
-template <int D, int KH>
+template <int D, int KH, bool RAGGED>
 static hipError_t launch_split_kh(const DecodeArgs& a, dim3 grid, uint32_t G, hipStream_t st) {
   switch (G) {
-#define FLK_CASE(g)                                                                             \
-  case g:                                                                                       \
-    hipLaunchKernelGGL((decode_split_kernel<D, g, KH>), grid, dim3(kDecodeThreads), 0, st, a); \
+#define FLK_CASE(g)                                                                      \
+  case g:                                                                                \
+    hipLaunchKernelGGL((decode_split_kernel<D, g, KH, RAGGED>), grid, dim3(kDecodeThreads), 0, \
+                       st, a);                                                           \
     break;
     FLK_CASE(1)
     FLK_CASE(2)
@@ -635,12 +646,20 @@ static hipError_t launch_split_kh(const DecodeArgs& a, dim3 grid, uint32_t G, hi
 
 template <int D>
 static hipError_t launch_split_d(const DecodeArgs& a, dim3 grid, uint32_t G, uint32_t KH,
-                                 hipStream_t st) {
+                                 bool ragged, hipStream_t st) {
+  if (ragged) {
+    switch (KH) {
+      case 8: return launch_split_kh<D, 8, true>(a, grid, G, st);
+      case 4: return launch_split_kh<D, 4, true>(a, grid, G, st);
+      case 2: return launch_split_kh<D, 2, true>(a, grid, G, st);
+      default: return launch_split_kh<D, 1, true>(a, grid, G, st);
+    }
+  }
   switch (KH) {
-    case 8: return launch_split_kh<D, 8>(a, grid, G, st);
-    case 4: return launch_split_kh<D, 4>(a, grid, G, st);
-    case 2: return launch_split_kh<D, 2>(a, grid, G, st);
-    default: return launch_split_kh<D, 1>(a, grid, G, st);
+    case 8: return launch_split_kh<D, 8, false>(a, grid, G, st);
+    case 4: return launch_split_kh<D, 4, false>(a, grid, G, st);
+    case 2: return launch_split_kh<D, 2, false>(a, grid, G, st);
+    default: return launch_split_kh<D, 1, false>(a, grid, G, st);
   }
 }
 
@@ -685,8 +704,9 @@ hipError_t launch_decode(const float* q, const float* kcache, const float* vcach
   const uint32_t KH = kv_heads_per_wg(s.n_kv_heads);
   const dim3 grid(s.n_kv_heads / KH, a.max_splits, s.n_seqs);
   const uint32_t G = s.n_heads / s.n_kv_heads;
-  hipError_t e = s.head_dim == 128 ? launch_split_d<128>(a, grid, G, KH, st)
-                                   : launch_split_d<64>(a, grid, G, KH, st);
+  const bool ragged = s.n_seqs > 1;  // the plan's kpi assumes the same instance
+  hipError_t e = s.head_dim == 128 ? launch_split_d<128>(a, grid, G, KH, ragged, st)
+                                   : launch_split_d<64>(a, grid, G, KH, ragged, st);
   if (e != hipSuccess || a.max_splits <= 1) return e;
   const dim3 mgrid(s.n_heads, s.head_dim / 4 / kMergeCols, s.n_seqs);
   if (s.head_dim == 128)
