@@ -417,10 +417,9 @@ def test_prefill_deterministic_across_runs(rng):
 
 
 # ------------------------------------------------------------------- ragged --
-def test_decode_ragged_matches_per_sequence_oracle(rng):
-    # Extension (no reference counterpart): independent sequences, one launch.
-    H, Hkv, d, B = 16, 8, 128, 9
-    lens = np.array([1, 5, 64, 65, 300, 1000, 2500, 0, 777], np.uint32)
+def _ragged_vs_oracle(rng, H, Hkv, d, lens):
+    lens = np.asarray(lens, np.uint32)
+    B = len(lens)
     offs = np.concatenate([[0], np.cumsum(lens + 3)[:-1]]).astype(np.uint64)  # gaps between seqs
     rows = int(offs[-1] + lens[-1] + 3)
     kc, vc = randn(rng, rows * Hkv * d), randn(rng, rows * Hkv * d)
@@ -433,14 +432,33 @@ def test_decode_ragged_matches_per_sequence_oracle(rng):
     row = Hkv * d
     for b in range(B):
         if lens[b] == 0:
-            assert np.all(got[b] == 0)
+            assert np.all(got[b] == 0), b
             continue
         s = int(offs[b]) * row
         qb = q[b * H * d:(b + 1) * H * d]
         kb, vb = kc[s:s + int(lens[b]) * row], vc[s:s + int(lens[b]) * row]
         want = oracle.attn(qb, kb, vb, H, Hkv, d, int(lens[b]))
         m = metrics(got[b], want, cf.attention(qb, kb, vb, H, Hkv, d, 1, int(lens[b]) - 1))
-        assert meets_bar(m), (b, fmt(m))
+        assert meets_bar(m), (b, int(lens[b]), fmt(m))
+
+
+# Every kv-heads-per-workgroup instance (8, 4, 2, 1), groups on both sides of
+# 4 (the batched instance keeps 4 keys per slot in flight up to G = 4, 2
+# above), both head sizes. Lengths sit at and around the instance's block of
+# keys per iteration: 512 / (d / 4) slots / KH kv heads x keys per slot.
+@pytest.mark.parametrize("H,Hkv,d", [(16, 8, 128), (16, 8, 64), (32, 8, 128), (64, 8, 64),
+                                     (4, 4, 128), (12, 4, 64), (10, 2, 128), (8, 1, 128),
+                                     (5, 1, 64), (15, 5, 128)])
+def test_decode_ragged_head_layouts(rng, H, Hkv, d):
+    G = H // Hkv
+    kh = next(k for k in (8, 4, 2, 1) if Hkv % k == 0)
+    kpi = (512 // (d // 4)) // kh * (4 if G <= 4 else 2)
+    _ragged_vs_oracle(rng, H, Hkv, d, [1, kpi - 1, kpi, kpi + 1, 2 * kpi + 3, 0, 1500])
+
+
+def test_decode_ragged_matches_per_sequence_oracle(rng):
+    # Extension (no reference counterpart): independent sequences, one launch.
+    _ragged_vs_oracle(rng, 16, 8, 128, [1, 5, 64, 65, 300, 1000, 2500, 0, 777])
 
 
 # ------------------------------------------------------------ golden fixtures --
