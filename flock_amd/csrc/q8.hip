@@ -64,7 +64,7 @@ constexpr int kQ8Threads = 256;   // 4 waves
 // row's sum and the norm's loads after the weights 30.98-31.00; residuals
 // requested with the weights 30.22-30.26; and the norm's first batch ahead of
 // the weights 29.40-29.51; the fused x and gain also requested before the
-// norm's reduction (one round trip fewer, 32 more registers) 29.65.
+// norm's reduction (one round trip fewer, 32 more registers) 29.65, not kept.
 #ifndef FLK_Q8_RES_EARLY
 #define FLK_Q8_RES_EARLY 1
 #endif
