@@ -82,7 +82,7 @@ class DeviceBuffer:
 
     def __del__(self):
         p = getattr(self, "ptr", None)
-        if p:
+        if p and _pending_free is not None:  # None while the interpreter shuts down
             _pending_free.append(p)
             self.ptr = None
 
