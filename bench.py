@@ -396,8 +396,8 @@ class Chunk32k(Prefill2k):
 
 class Ragged(Workload):
     name = "ragged"
-    kernel = ("flk_attn_decode_ragged: decode_split_kernel<128,2,8> + "
-              "decode_merge_kernel<128>")
+    kernel = ("flk_attn_decode_ragged: queue_zero_kernel + decode_batch_kernel<128,2,8> "
+              "(persistent, claimed items) + decode_merge_kernel<128>")
 
     def __init__(self, torch, ops, n_seqs=64, seed=3):
         self.torch, self.ops = torch, ops

@@ -94,6 +94,9 @@ constexpr int kMergeBatch = 8;   // splits per thread per round of loads
 // latency) keep more rows in flight: 64 sequences, 1025..16385 keys, 731 ->
 // 712 us per call with 4 instead of 2; one 32769-key sequence is slower
 // with 4 (45.4 -> 47.2 us per fused call).
+#ifndef FLK_DECODE_BATCH
+#define FLK_DECODE_BATCH 1  // ragged batches of up to kBatchMaxSeqs: persistent decode_batch_kernel
+#endif
 #ifndef FLK_DECODE_RAGGED_UNROLL
 #define FLK_DECODE_RAGGED_UNROLL 4
 #endif
@@ -208,6 +211,55 @@ __device__ __forceinline__ void attend_keys(const float4 (&kr_in)[U], const floa
       acc[g].w = fmaf(e, vr[u].w, acc[g].w);
     }
     m[g] = mn;
+  }
+}
+
+// The key phases of each kv head combined through LDS (PH > 1), then emit(hq,
+// c, M, L, A) for every (q head of the workgroup, float4 column). Every
+// thread of the workgroup calls it.
+template <int D, int G, int KH, int PH, class EMIT>
+__device__ __forceinline__ void combine_phases(const float (&m)[G], const float (&l)[G],
+                                               const float4 (&acc)[G], int slot, int sl, int kh,
+                                               int tid, float (*s_m)[G], float (*s_l)[G],
+                                               float4 (*s_acc)[G][D / 4], EMIT emit) {
+  constexpr int LPK = D / 4;
+  constexpr int HG = KH * G;
+  if constexpr (PH == 1) {
+#pragma unroll
+    for (int g = 0; g < G; g++) emit(kh * G + g, sl, m[g], l[g], acc[g]);
+    return;
+  }
+  if (sl == 0) {
+#pragma unroll
+    for (int g = 0; g < G; g++) {
+      s_m[slot][g] = m[g];
+      s_l[slot][g] = l[g];
+    }
+  }
+#pragma unroll
+  for (int g = 0; g < G; g++) s_acc[slot][g][sl] = acc[g];
+  __syncthreads();
+  for (int i = tid; i < HG * LPK; i += kDecodeThreads) {
+    const int hq = i / LPK, c = i % LPK;  // hq = kv-head-in-group * G + g
+    const int j = hq / G, g = hq % G;
+    float M = -INFINITY;
+#pragma unroll
+    for (int p = 0; p < PH; p++) M = fmaxf(M, s_m[j + KH * p][g]);
+    float L = 0.f;
+    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll
+    for (int p = 0; p < PH; p++) {
+      const int sidx = j + KH * p;
+      const float ms = s_m[sidx][g];
+      const float w = ms == -INFINITY ? 0.f : expf(ms - M);
+      L = fmaf(s_l[sidx][g], w, L);
+      const float4 as = s_acc[sidx][g][c];
+      A.x = fmaf(as.x, w, A.x);
+      A.y = fmaf(as.y, w, A.y);
+      A.z = fmaf(as.z, w, A.z);
+      A.w = fmaf(as.w, w, A.w);
+    }
+    emit(hq, c, M, L, A);
   }
 }
 
@@ -398,42 +450,201 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs
       reinterpret_cast<float4*>(a.part_acc + p * D)[c] = A;
     }
   };
-  if (PH == 1) {
+  combine_phases<D, G, KH, PH>(m, l, acc, slot, sl, kh, tid, s_m, s_l, s_acc, emit);
+}
+
+// ------------------------------------------------------- ragged batches ----
+// decode_batch_kernel<D, G, KH>  grid (n_kv_heads / KH, kBatchWG / groups),
+//   512 threads: the same splits, partials and merge as decode_split_kernel's
+//   ragged instance, run by one long-lived workgroup per CU instead of one
+//   workgroup per split (a bare read of 4 GiB in this shape: 610 us, against
+//   660-664 us as ~4000 one-shot workgroups). The batch's (sequence, split)
+//   items are numbered sequence by sequence (an empty sequence has one item,
+//   which zeroes its rows) and claimed in order from a counter (one per kv
+//   head group, zeroed by queue_zero_kernel at the start of the call), so at
+//   any time the workgroups sweep a few sequences, each as a moving window,
+//   and a faster XCD simply claims more items (a fixed stride of items per
+//   workgroup measured 728-733 us, slower than one-shot workgroups at 710, as
+//   the slowest XCD then sets the end). Which workgroup runs an item does not
+//   change its partial, so results are bit-reproducible. Each workgroup first
+//   builds, in LDS, the first item of every sequence (a prefix sum of the
+//   split counts) and the sequences' key counts and row offsets.
+#ifndef FLK_DECODE_BATCH_WG
+#define FLK_DECODE_BATCH_WG 256
+#endif
+constexpr uint32_t kBatchWG = FLK_DECODE_BATCH_WG;
+constexpr uint32_t kBatchMaxSeqs = 2048;
+
+constexpr uint32_t kBatchMaxGroups = 64;  // item counters in the workspace
+constexpr uint64_t kQueueBytes = 256;      // kBatchMaxGroups counters, 256-byte aligned
+
+// Whether a batch of n_seqs sequences in `groups` kv-head groups takes
+// decode_batch_kernel (its tables fit in LDS, its counters in kQueueBytes).
+static bool use_batch(uint32_t n_seqs, uint32_t groups) {
+  return FLK_DECODE_BATCH && n_seqs <= kBatchMaxSeqs && groups <= kBatchMaxGroups;
+}
+
+__global__ void queue_zero_kernel(uint32_t* queue, uint32_t n) {
+  if (threadIdx.x < n) queue[threadIdx.x] = 0u;
+}
+
+template <int D, int G, int KH>
+__global__ __launch_bounds__(kDecodeThreads) void decode_batch_kernel(DecodeArgs a,
+                                                                      uint32_t n_seqs,
+                                                                      uint32_t* queue) {
+  constexpr int LPK = D / 4;
+  constexpr int SLOTS = kDecodeThreads / LPK;
+  static_assert(SLOTS % KH == 0, "KH must divide the slot count");
+  constexpr int PH = SLOTS / KH;
+  constexpr int U = decode_unroll(G, true);
+  constexpr int KPI = PH * U;
+  constexpr int HG = KH * G;
+  constexpr int WAVES = kDecodeThreads / kWave;
+
+  __shared__ float4 s_q[HG][LPK];
+  __shared__ float s_m[PH > 1 ? SLOTS : 1][G];
+  __shared__ float s_l[PH > 1 ? SLOTS : 1][G];
+  __shared__ float4 s_acc[PH > 1 ? SLOTS : 1][G][LPK];
+  __shared__ uint32_t s_first[kBatchMaxSeqs + 1];  // first item of each sequence
+  __shared__ uint32_t s_nk[kBatchMaxSeqs];
+  __shared__ uint64_t s_row[kBatchMaxSeqs];
+  __shared__ uint32_t s_wsum[WAVES];
+  __shared__ uint32_t s_item;
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int slot = tid / LPK;
+  const int sl = tid % LPK;
+  const int kh = slot % KH;
+  const int ph = slot / KH;
+  const uint32_t kvh0 = blockIdx.x * KH;
+  const uint32_t kvh = kvh0 + kh;
+  const uint32_t h0 = kvh0 * G;
+  const size_t row4 = (size_t)a.n_kv_heads * (D / 4);
+
+  // ---- item table: exclusive prefix of items per sequence, 512 at a time --
+  uint32_t carry = 0;
+  for (uint32_t c0 = 0; c0 < n_seqs; c0 += kDecodeThreads) {
+    const uint32_t sq = c0 + tid;
+    uint32_t items = 0;
+    if (sq < n_seqs) {
+      const uint32_t nk = seq_keys(a, sq);
+      s_nk[sq] = nk;
+      s_row[sq] = a.seq_row_off[sq];
+      items = nk == 0 ? 1u : seq_splits(a, nk);
+    }
+    uint32_t incl = items;  // inclusive scan over the wave
 #pragma unroll
-    for (int g = 0; g < G; g++) emit(kh * G + g, sl, m[g], l[g], acc[g]);
-    return;
+    for (int d = 1; d < kWave; d <<= 1) {
+      const uint32_t o = (uint32_t)__shfl_up((int)incl, d, kWave);
+      if (lane >= d) incl += o;
+    }
+    if (lane == kWave - 1) s_wsum[wave] = incl;
+    __syncthreads();
+    uint32_t before = carry;
+    for (int w = 0; w < wave; w++) before += s_wsum[w];
+    if (sq < n_seqs) s_first[sq] = before + incl - items;
+    for (int w = 0; w < WAVES; w++) carry += s_wsum[w];
+    __syncthreads();
   }
-  if (sl == 0) {
+  if (tid == 0) s_first[n_seqs] = carry;
+  __syncthreads();
+  const uint32_t n_items = carry;
+
+  // One (sequence, split) item of a non-empty sequence; the workgroup's
+  // threads all call it (barriers inside).
+  auto attend_item = [&](uint32_t seq, uint32_t split, uint32_t n_keys) {
+    const uint32_t n_splits = s_first[seq + 1] - s_first[seq];
+    const uint32_t n_blocks = (n_keys + KPI - 1) / KPI;
+    const uint32_t t1 = n_keys;
+    const uint64_t row0 = s_row[seq];
+
+    constexpr int QLD = (HG * LPK + kDecodeThreads - 1) / kDecodeThreads;
+    float4 qld[QLD];
+    {
+      const float4* qs = reinterpret_cast<const float4*>(a.q + ((size_t)seq * a.n_heads + h0) * D);
+#pragma unroll
+      for (int i = 0; i < QLD; i++) qld[i] = qs[min(tid + kDecodeThreads * i, HG * LPK - 1)];
+    }
+    const size_t col = (size_t)kvh * LPK + sl;
+    const float4* kb = reinterpret_cast<const float4*>(a.kcache) + row0 * row4 + col;
+    const float4* vb = reinterpret_cast<const float4*>(a.vcache) + row0 * row4 + col;
+    float4 ka[U], va[U], kn[U], vn[U];
+    load_keys<U, PH>(ka, va, kb, vb, row4, split * KPI, ph, t1);
+#pragma unroll
+    for (int i = 0; i < QLD; i++) {
+      const int f = min(tid + kDecodeThreads * i, HG * LPK - 1);
+      s_q[f / LPK][f % LPK] = qld[i];
+    }
+    __syncthreads();  // s_q ready (the previous item's LDS reads are done)
+    float4 qv[G];
+#pragma unroll
+    for (int g = 0; g < G; g++) qv[g] = s_q[kh * G + g][sl];
+    float m[G], l[G];
+    float4 acc[G];
 #pragma unroll
     for (int g = 0; g < G; g++) {
-      s_m[slot][g] = m[g];
-      s_l[slot][g] = l[g];
+      m[g] = -INFINITY;
+      l[g] = 0.f;
+      acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-  }
-#pragma unroll
-  for (int g = 0; g < G; g++) s_acc[slot][g][sl] = acc[g];
+    const float4 none = make_float4(0.f, 0.f, 0.f, 0.f);
+    for (uint32_t b = split; b < n_blocks; b += 2 * n_splits) {
+      const uint32_t b1 = b + n_splits;
+      const uint32_t b2 = b1 + n_splits;
+      load_keys<U, PH>(kn, vn, kb, vb, row4, (b1 < n_blocks ? b1 : 0) * KPI, ph, t1);
+      attend_keys<D, G, U, PH>(ka, va, qv, m, l, acc, b * KPI, ph, t1, false, 0, none, none,
+                               a.scale);
+      load_keys<U, PH>(ka, va, kb, vb, row4, (b2 < n_blocks ? b2 : 0) * KPI, ph, t1);
+      if (b1 < n_blocks)
+        attend_keys<D, G, U, PH>(kn, vn, qv, m, l, acc, b1 * KPI, ph, t1, false, 0, none, none,
+                                 a.scale);
+    }
+    auto emit = [&](int hq, int c, float M, float L, float4 A) {
+      const uint32_t h = h0 + (uint32_t)hq;
+      if (n_splits == 1) {
+        reinterpret_cast<float4*>(a.o + ((size_t)seq * a.n_heads + h) * D)[c] =
+            make_float4(A.x / L, A.y / L, A.z / L, A.w / L);
+      } else {
+        const size_t p = ((size_t)seq * a.n_heads + h) * a.max_splits + split;
+        if (c == 0) a.part_ml[p] = make_float2(M, L);
+        reinterpret_cast<float4*>(a.part_acc + p * D)[c] = A;
+      }
+    };
+    combine_phases<D, G, KH, PH>(m, l, acc, slot, sl, kh, tid, s_m, s_l, s_acc, emit);
+  };
+
+  // Items are claimed one ahead: the claim of the next item is issued when
+  // this one starts, so its round trip overlaps the item's work.
+  uint32_t* counter = queue + blockIdx.x;
+  if (tid == 0)
+    s_item = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
-  for (int i = tid; i < HG * LPK; i += kDecodeThreads) {
-    const int hq = i / LPK, c = i % LPK;  // hq = kv-head-in-group * G + g
-    const int j = hq / G, g = hq % G;
-    float M = -INFINITY;
-#pragma unroll
-    for (int p = 0; p < PH; p++) M = fmaxf(M, s_m[j + KH * p][g]);
-    float L = 0.f;
-    float4 A = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll
-    for (int p = 0; p < PH; p++) {
-      const int sidx = j + KH * p;
-      const float ms = s_m[sidx][g];
-      const float w = ms == -INFINITY ? 0.f : expf(ms - M);
-      L = fmaf(s_l[sidx][g], w, L);
-      const float4 as = s_acc[sidx][g][c];
-      A.x = fmaf(as.x, w, A.x);
-      A.y = fmaf(as.y, w, A.y);
-      A.z = fmaf(as.z, w, A.z);
-      A.w = fmaf(as.w, w, A.w);
+  uint32_t it = s_item;
+  while (it < n_items) {
+    uint32_t nxt = 0;
+    if (tid == 0)
+      nxt = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    // The item's sequence: the last seq with s_first[seq] <= it.
+    uint32_t lo = 0, hi = n_seqs;  // s_first[lo] <= it < s_first[hi]
+    while (hi - lo > 1) {
+      const uint32_t mid = (lo + hi) / 2;
+      if (s_first[mid] <= it) lo = mid; else hi = mid;
     }
-    emit(hq, c, M, L, A);
+    const uint32_t seq = lo;
+    const uint32_t split = it - s_first[seq];
+    const uint32_t n_keys = s_nk[seq];
+    if (n_keys == 0) {  // empty sequence: zero rows
+      for (int i = tid; i < HG * D; i += kDecodeThreads)
+        a.o[((size_t)seq * a.n_heads + h0) * D + i] = 0.f;
+    } else {
+      attend_item(seq, split, n_keys);
+    }
+    if (tid == 0) s_item = nxt;
+    __syncthreads();
+    it = s_item;
+    __syncthreads();  // every thread has read s_item before it is written again
   }
 }
 
@@ -598,7 +809,9 @@ static uint64_t ws_for_slots(uint64_t slots, uint32_t head_dim) {
 uint64_t decode_ws_bytes(const DecodeShape& s) {
   const SplitPlan p = split_plan(s);
   if (p.max_splits <= 1) return 0;
-  return ws_for_slots((uint64_t)s.n_seqs * s.n_heads * p.max_splits, s.head_dim);
+  const uint32_t groups = s.n_kv_heads / kv_heads_per_wg(s.n_kv_heads);
+  const uint64_t queue = s.n_seqs > 1 && use_batch(s.n_seqs, groups) ? kQueueBytes : 0;
+  return queue + ws_for_slots((uint64_t)s.n_seqs * s.n_heads * p.max_splits, s.head_dim);
 }
 
 // Bound over every call with n_keys <= s.max_n_keys and n_seqs <= s.n_seqs
@@ -618,7 +831,8 @@ uint64_t decode_ws_bound(const DecodeShape& s) {
     const uint64_t splits = by_len < by_wg ? by_len : by_wg;
     if (splits > 1 && n * splits > best) best = n * splits;
   }
-  return best ? ws_for_slots(best * s.n_heads, s.head_dim) : 0;
+  // (+ the batch kernel's counters, which only calls of 2+ sequences use)
+  return best ? kQueueBytes + ws_for_slots(best * s.n_heads, s.head_dim) : 0;
 }
 
 template <int D, int KH, bool RAGGED>
@@ -642,6 +856,41 @@ static hipError_t launch_split_kh(const DecodeArgs& a, dim3 grid, uint32_t G, hi
       return hipErrorInvalidValue;
   }
   return hipGetLastError();
+}
+
+template <int D, int KH>
+static hipError_t launch_batch_kh(const DecodeArgs& a, dim3 grid, uint32_t G, uint32_t n_seqs,
+                                  uint32_t* queue, hipStream_t st) {
+  switch (G) {
+#define FLK_CASE(g)                                                                          \
+  case g:                                                                                    \
+    hipLaunchKernelGGL((decode_batch_kernel<D, g, KH>), grid, dim3(kDecodeThreads), 0, st, a, \
+                       n_seqs, queue);                                                       \
+    break;
+    FLK_CASE(1)
+    FLK_CASE(2)
+    FLK_CASE(3)
+    FLK_CASE(4)
+    FLK_CASE(5)
+    FLK_CASE(6)
+    FLK_CASE(7)
+    FLK_CASE(8)
+#undef FLK_CASE
+    default:
+      return hipErrorInvalidValue;
+  }
+  return hipGetLastError();
+}
+
+template <int D>
+static hipError_t launch_batch_d(const DecodeArgs& a, dim3 grid, uint32_t G, uint32_t KH,
+                                 uint32_t n_seqs, uint32_t* queue, hipStream_t st) {
+  switch (KH) {
+    case 8: return launch_batch_kh<D, 8>(a, grid, G, n_seqs, queue, st);
+    case 4: return launch_batch_kh<D, 4>(a, grid, G, n_seqs, queue, st);
+    case 2: return launch_batch_kh<D, 2>(a, grid, G, n_seqs, queue, st);
+    default: return launch_batch_kh<D, 1>(a, grid, G, n_seqs, queue, st);
+  }
 }
 
 template <int D>
@@ -682,8 +931,15 @@ hipError_t launch_decode(const float* q, const float* kcache, const float* vcach
   a.bps = plan.bps;
   a.max_splits = plan.max_splits;
   a.scale = (float)(1.0 / sqrt((double)s.head_dim));
+  const uint32_t KH = kv_heads_per_wg(s.n_kv_heads);
+  const uint32_t groups = s.n_kv_heads / KH;
+  const bool ragged = s.n_seqs > 1;  // the plan's kpi assumes the same instance
+  // Batches take the claimed-item kernel when they have partials (so a
+  // workspace, whose first kQueueBytes hold its counters).
+  const bool batch = ragged && use_batch(s.n_seqs, groups) && a.max_splits > 1;
+  uint32_t* queue = batch ? static_cast<uint32_t*>(ws) : nullptr;
   if (a.max_splits > 1) {
-    char* w = static_cast<char*>(ws);
+    char* w = static_cast<char*>(ws) + (batch ? kQueueBytes : 0);
     const uint64_t slots = (uint64_t)s.n_seqs * s.n_heads * a.max_splits;
     a.part_ml = reinterpret_cast<float2*>(w);
     a.part_acc = reinterpret_cast<float*>(w + ws_align(slots * sizeof(float2)));
@@ -701,12 +957,20 @@ hipError_t launch_decode(const float* q, const float* kcache, const float* vcach
     a.kcache_w = fused->kcache_w;
     a.vcache_w = fused->vcache_w;
   }
-  const uint32_t KH = kv_heads_per_wg(s.n_kv_heads);
-  const dim3 grid(s.n_kv_heads / KH, a.max_splits, s.n_seqs);
+  const dim3 grid(groups, a.max_splits, s.n_seqs);
   const uint32_t G = s.n_heads / s.n_kv_heads;
-  const bool ragged = s.n_seqs > 1;  // the plan's kpi assumes the same instance
-  hipError_t e = s.head_dim == 128 ? launch_split_d<128>(a, grid, G, KH, ragged, st)
-                                   : launch_split_d<64>(a, grid, G, KH, ragged, st);
+  hipError_t e;
+  if (batch) {
+    // The counters start at zero: a kernel, not a memset, so that a captured
+    // graph replays it.
+    hipLaunchKernelGGL(queue_zero_kernel, dim3(1), dim3(kBatchMaxGroups), 0, st, queue, groups);
+    const dim3 bgrid(groups, kBatchWG / groups > 0 ? kBatchWG / groups : 1);
+    e = s.head_dim == 128 ? launch_batch_d<128>(a, bgrid, G, KH, s.n_seqs, queue, st)
+                          : launch_batch_d<64>(a, bgrid, G, KH, s.n_seqs, queue, st);
+  } else {
+    e = s.head_dim == 128 ? launch_split_d<128>(a, grid, G, KH, ragged, st)
+                          : launch_split_d<64>(a, grid, G, KH, ragged, st);
+  }
   if (e != hipSuccess || a.max_splits <= 1) return e;
   const dim3 mgrid(s.n_heads, s.head_dim / 4 / kMergeCols, s.n_seqs);
   if (s.head_dim == 128)

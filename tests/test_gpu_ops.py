@@ -461,6 +461,31 @@ def test_decode_ragged_matches_per_sequence_oracle(rng):
     _ragged_vs_oracle(rng, 16, 8, 128, [1, 5, 64, 65, 300, 1000, 2500, 0, 777])
 
 
+def test_decode_ragged_repeats_bit_for_bit(rng):
+    # The batch's (sequence, split) items are claimed by whichever workgroup
+    # is free; every item still writes its own partial, so repeated calls on
+    # one workspace (whose item counters each call resets) agree bit for bit,
+    # also after the workspace has served a prefill in between.
+    H, Hkv, d = 16, 8, 128
+    lens = np.array([3000, 1, 0, 4097, 700, 2048, 33, 1500], np.uint32)
+    B = len(lens)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
+    rows = int(lens.sum())
+    kc, vc, q = dev(randn(rng, rows * Hkv * d)), dev(randn(rng, rows * Hkv * d)), dev(randn(rng, B * H * d))
+    offs_d, lens_d = ops.DeviceBuffer.from_array(offs), ops.DeviceBuffer.from_array(lens)
+    maxn = int(lens.max())
+    ws = ops.Workspace(H, Hkv, d, maxn, 64, B)
+    o = empty(B * H * d)
+    outs = []
+    for i in range(5):
+        if i == 3:  # the workspace serves a 64-query prefill in between
+            pq, po = dev(randn(rng, 64 * H * d)), empty(64 * H * d)
+            ops.attn_prefill(pq, kc, vc, po, H, Hkv, d, 64, 2000, ws)
+        ops.attn_decode_ragged(q, kc, vc, offs_d, lens_d, o, B, maxn, H, Hkv, d, ws)
+        outs.append(get(o, B * H * d))
+    assert all(np.array_equal(x, outs[0]) for x in outs[1:])
+
+
 # ------------------------------------------------------------ golden fixtures --
 def test_golden_fixtures_on_gpu():
     # tests/golden/golden.npz: seeded inputs with the oracle's outputs and the
