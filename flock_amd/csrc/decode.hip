@@ -552,35 +552,91 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_batch_kernel(DecodeArgs
   __syncthreads();
   const uint32_t n_items = carry;
 
-  // One (sequence, split) item of a non-empty sequence; the workgroup's
-  // threads all call it (barriers inside).
-  auto attend_item = [&](uint32_t seq, uint32_t split, uint32_t n_keys) {
+  // Item -> (sequence, split, keys): the last sequence whose first item is
+  // at or before it (every sequence has at least one item).
+  auto locate = [&](uint32_t item, uint32_t& seq, uint32_t& split, uint32_t& n_keys) {
+    uint32_t lo = 0, hi = n_seqs;  // s_first[lo] <= item < s_first[hi]
+    while (hi - lo > 1) {
+      const uint32_t mid = (lo + hi) / 2;
+      if (s_first[mid] <= item) lo = mid; else hi = mid;
+    }
+    seq = lo;
+    split = item - s_first[lo];
+    n_keys = s_nk[lo];
+  };
+  const size_t col = (size_t)kvh * LPK + sl;
+  auto k_base = [&](uint32_t seq) {
+    return reinterpret_cast<const float4*>(a.kcache) + s_row[seq] * row4 + col;
+  };
+  auto v_base = [&](uint32_t seq) {
+    return reinterpret_cast<const float4*>(a.vcache) + s_row[seq] * row4 + col;
+  };
+  constexpr int QLD = (HG * LPK + kDecodeThreads - 1) / kDecodeThreads;
+  auto load_q = [&](uint32_t seq, float4 (&qld)[QLD]) {
+    const float4* qs = reinterpret_cast<const float4*>(a.q + ((size_t)seq * a.n_heads + h0) * D);
+#pragma unroll
+    for (int i = 0; i < QLD; i++) qld[i] = qs[min(tid + kDecodeThreads * i, HG * LPK - 1)];
+  };
+
+  // Items are claimed one ahead: the claim of the next item is issued as an
+  // item starts and published at its first barrier; the item's last
+  // iteration then loads the next item's first block (in place of the
+  // unused reload every split's last iteration makes) and its q is requested
+  // before the combine, so a new item starts with its data in registers.
+  uint32_t* counter = queue + blockIdx.x;
+  if (tid == 0)
+    s_item = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+  __syncthreads();
+  uint32_t it = s_item;
+  bool pre = false;  // ka, va and qld hold item it's first block and q
+  float4 ka[U], va[U], kn[U], vn[U];
+  float4 qld[QLD];
+  const float4 none = make_float4(0.f, 0.f, 0.f, 0.f);
+  while (it < n_items) {
+    uint32_t claim = 0;
+    if (tid == 0)
+      claim = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+    uint32_t seq, split, n_keys;
+    locate(it, seq, split, n_keys);
+    if (n_keys == 0) {  // empty sequence: zero rows
+      for (int i = tid; i < HG * D; i += kDecodeThreads)
+        a.o[((size_t)seq * a.n_heads + h0) * D + i] = 0.f;
+      if (tid == 0) s_item = claim;
+      __syncthreads();
+      it = s_item;
+      pre = false;
+      __syncthreads();  // every thread has read s_item before it is written again
+      continue;         // uniform
+    }
     const uint32_t n_splits = s_first[seq + 1] - s_first[seq];
     const uint32_t n_blocks = (n_keys + KPI - 1) / KPI;
     const uint32_t t1 = n_keys;
-    const uint64_t row0 = s_row[seq];
-
-    constexpr int QLD = (HG * LPK + kDecodeThreads - 1) / kDecodeThreads;
-    float4 qld[QLD];
-    {
-      const float4* qs = reinterpret_cast<const float4*>(a.q + ((size_t)seq * a.n_heads + h0) * D);
-#pragma unroll
-      for (int i = 0; i < QLD; i++) qld[i] = qs[min(tid + kDecodeThreads * i, HG * LPK - 1)];
+    const float4* kb = k_base(seq);
+    const float4* vb = v_base(seq);
+    if (!pre) {
+      load_q(seq, qld);
+      load_keys<U, PH>(ka, va, kb, vb, row4, split * KPI, ph, t1);
     }
-    const size_t col = (size_t)kvh * LPK + sl;
-    const float4* kb = reinterpret_cast<const float4*>(a.kcache) + row0 * row4 + col;
-    const float4* vb = reinterpret_cast<const float4*>(a.vcache) + row0 * row4 + col;
-    float4 ka[U], va[U], kn[U], vn[U];
-    load_keys<U, PH>(ka, va, kb, vb, row4, split * KPI, ph, t1);
 #pragma unroll
     for (int i = 0; i < QLD; i++) {
       const int f = min(tid + kDecodeThreads * i, HG * LPK - 1);
       s_q[f / LPK][f % LPK] = qld[i];
     }
-    __syncthreads();  // s_q ready (the previous item's LDS reads are done)
+    if (tid == 0) s_item = claim;
+    __syncthreads();  // s_q and the next item ready (the previous item's LDS reads are done)
+    const uint32_t nit = s_item;
     float4 qv[G];
 #pragma unroll
     for (int g = 0; g < G; g++) qv[g] = s_q[kh * G + g][sl];
+    // The next item, if it has keys: where its first block is.
+    uint32_t nseq = seq, nsplit = 0, nkeys = 0;
+    if (nit < n_items) locate(nit, nseq, nsplit, nkeys);
+    const bool pf = nit < n_items && nkeys > 0;
+    const float4* nkb = pf ? k_base(nseq) : kb;
+    const float4* nvb = pf ? v_base(nseq) : vb;
+    const uint32_t nbase = pf ? nsplit * KPI : 0;
+    const uint32_t nt1 = pf ? nkeys : t1;
+
     float m[G], l[G];
     float4 acc[G];
 #pragma unroll
@@ -589,18 +645,21 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_batch_kernel(DecodeArgs
       l[g] = 0.f;
       acc[g] = make_float4(0.f, 0.f, 0.f, 0.f);
     }
-    const float4 none = make_float4(0.f, 0.f, 0.f, 0.f);
     for (uint32_t b = split; b < n_blocks; b += 2 * n_splits) {
       const uint32_t b1 = b + n_splits;
       const uint32_t b2 = b1 + n_splits;
       load_keys<U, PH>(kn, vn, kb, vb, row4, (b1 < n_blocks ? b1 : 0) * KPI, ph, t1);
       attend_keys<D, G, U, PH>(ka, va, qv, m, l, acc, b * KPI, ph, t1, false, 0, none, none,
                                a.scale);
-      load_keys<U, PH>(ka, va, kb, vb, row4, (b2 < n_blocks ? b2 : 0) * KPI, ph, t1);
+      if (b2 < n_blocks)
+        load_keys<U, PH>(ka, va, kb, vb, row4, b2 * KPI, ph, t1);
+      else  // the last iteration: the next item's first block (or a reload)
+        load_keys<U, PH>(ka, va, nkb, nvb, row4, nbase, ph, nt1);
       if (b1 < n_blocks)
         attend_keys<D, G, U, PH>(kn, vn, qv, m, l, acc, b1 * KPI, ph, t1, false, 0, none, none,
                                  a.scale);
     }
+    if (pf) load_q(nseq, qld);
     auto emit = [&](int hq, int c, float M, float L, float4 A) {
       const uint32_t h = h0 + (uint32_t)hq;
       if (n_splits == 1) {
@@ -613,38 +672,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_batch_kernel(DecodeArgs
       }
     };
     combine_phases<D, G, KH, PH>(m, l, acc, slot, sl, kh, tid, s_m, s_l, s_acc, emit);
-  };
-
-  // Items are claimed one ahead: the claim of the next item is issued when
-  // this one starts, so its round trip overlaps the item's work.
-  uint32_t* counter = queue + blockIdx.x;
-  if (tid == 0)
-    s_item = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-  __syncthreads();
-  uint32_t it = s_item;
-  while (it < n_items) {
-    uint32_t nxt = 0;
-    if (tid == 0)
-      nxt = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
-    // The item's sequence: the last seq with s_first[seq] <= it.
-    uint32_t lo = 0, hi = n_seqs;  // s_first[lo] <= it < s_first[hi]
-    while (hi - lo > 1) {
-      const uint32_t mid = (lo + hi) / 2;
-      if (s_first[mid] <= it) lo = mid; else hi = mid;
-    }
-    const uint32_t seq = lo;
-    const uint32_t split = it - s_first[seq];
-    const uint32_t n_keys = s_nk[seq];
-    if (n_keys == 0) {  // empty sequence: zero rows
-      for (int i = tid; i < HG * D; i += kDecodeThreads)
-        a.o[((size_t)seq * a.n_heads + h0) * D + i] = 0.f;
-    } else {
-      attend_item(seq, split, n_keys);
-    }
-    if (tid == 0) s_item = nxt;
-    __syncthreads();
-    it = s_item;
-    __syncthreads();  // every thread has read s_item before it is written again
+    __syncthreads();  // LDS (s_q, s_item, the combine) free for the next item
+    it = nit;
+    pre = pf;
   }
 }
 
