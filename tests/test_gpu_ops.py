@@ -461,6 +461,16 @@ def test_decode_ragged_matches_per_sequence_oracle(rng):
     _ragged_vs_oracle(rng, 16, 8, 128, [1, 5, 64, 65, 300, 1000, 2500, 0, 777])
 
 
+# Batches of up to 2048 sequences run on the persistent kernel (its tables
+# live in LDS); bigger ones on one workgroup per split. Both sides of the
+# boundary, with empty and one-key sequences among them.
+@pytest.mark.parametrize("n_seqs", [2048, 2100])
+def test_decode_ragged_many_sequences(rng, n_seqs):
+    lens = rng.integers(0, 41, n_seqs).astype(np.uint32)
+    lens[:3] = [0, 1, 40]
+    _ragged_vs_oracle(rng, 16, 8, 128, lens)
+
+
 def test_decode_ragged_repeats_bit_for_bit(rng):
     # The batch's (sequence, split) items are claimed by whichever workgroup
     # is free; every item still writes its own partial, so repeated calls on
