@@ -72,8 +72,13 @@ struct DecodeArgs {
 #ifndef FLK_DECODE_TARGET_WG
 #define FLK_DECODE_TARGET_WG 256
 #endif
+// Ragged batches: splits planned as if the longest sequence filled the batch
+// with this many split workgroups. On the persistent batch kernel, 64
+// sequences of 1025..16385 keys: 1024 739 us, 1536 690, 2048 676-677, 2560
+// 669-671, 3072 671-676, 4096 682, 6144 701-702, 8192 703, 12288 730 (more
+// items cost more per item than they save at the end of the queue).
 #ifndef FLK_DECODE_RAGGED_TARGET_WG
-#define FLK_DECODE_RAGGED_TARGET_WG 4096
+#define FLK_DECODE_RAGGED_TARGET_WG 3072
 #endif
 #ifndef FLK_DECODE_NT
 #define FLK_DECODE_NT 1  // K/V rows are read with the non-temporal hint (0: plain loads)
