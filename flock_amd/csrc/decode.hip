@@ -2,9 +2,10 @@
 //
 // The reference kernel (attention.wgsl:58-122) runs one 128-thread workgroup
 // per q-head and holds every score in workgroup memory, which caps context at
-// $MAX_KEYS and leaves the GPU with 16 workgroups. Here two launches:
+// $MAX_KEYS and leaves the GPU with 16 workgroups. Here two launches (three
+// for a ragged batch):
 //
-// decode_split_kernel<D, G, KH>  grid (n_kv_heads / KH, n_splits, n_seqs),
+// decode_split_kernel<D, G, KH, RAGGED>  grid (n_kv_heads / KH, n_splits, n_seqs),
 //   512 threads. A workgroup streams a share of the keys of KH adjacent kv heads and
 //   serves the KH * G query heads that read them (G = n_heads / n_kv_heads),
 //   so each K/V byte is read from HBM once. The cache row of one (key, kv head)
@@ -23,10 +24,13 @@
 //   accumulator) per slot; phases of one kv head merge through LDS. A
 //   single-split sequence writes o directly, otherwise each head writes its
 //   (m, l, acc) partial.
+// decode_batch_kernel<D, G, KH>  (ragged batches of up to 2048 sequences, after
+//   queue_zero_kernel): the same splits and partials, run by one persistent
+//   workgroup per CU that claims (sequence, split) items from a counter.
 // decode_merge_kernel  grid (n_heads, D / 32, n_seqs): combines the partials of
 //   one head with log-sum-exp weights in one round of loads.
-// The two launches are ordered by the stream: no atomics or device-scope fences
-// inside a launch.
+// The launches are ordered by the stream: no device-scope fences inside a
+// launch (the batch kernel's only atomics are its item claims).
 //
 // Fused mode (flk_decode_layer) prepends Layer.encode's prologue
 // (layer.ts:598-622): every workgroup computes q's per-head RMSNorm + RoPE for
