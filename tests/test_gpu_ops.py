@@ -471,6 +471,42 @@ def test_decode_ragged_many_sequences(rng, n_seqs):
     _ragged_vs_oracle(rng, 16, 8, 128, lens)
 
 
+def test_decode_ragged_graph_replay(rng):
+    # A captured ragged call replays its item-counter reset (a kernel, not a
+    # memset), so every replay gives the eager call's bits; eager calls in
+    # between leave the counters anywhere.
+    H, Hkv, d = 16, 8, 128
+    lens = np.array([2500, 0, 900, 4097, 1], np.uint32)
+    B = len(lens)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
+    rows = int(lens.sum())
+    kc, vc, q = dev(randn(rng, rows * Hkv * d)), dev(randn(rng, rows * Hkv * d)), dev(randn(rng, B * H * d))
+    offs_d, lens_d = ops.DeviceBuffer.from_array(offs), ops.DeviceBuffer.from_array(lens)
+    maxn = int(lens.max())
+    ws = ops.Workspace(H, Hkv, d, maxn, 0, B)
+    o = empty(B * H * d)
+    call = lambda: ops.attn_decode_ragged(q, kc, vc, offs_d, lens_d, o, B, maxn, H, Hkv, d, ws)
+    st = ops.Stream()
+    ops.set_stream(st)
+    try:
+        call()
+        ops.sync()
+        eager = get(o, B * H * d)
+        with ops.Graph() as g:
+            call()
+        for i in range(3):
+            o.zero()  # eager, between replays
+            g.launch()
+            ops.sync()
+            assert np.array_equal(get(o, B * H * d), eager), i
+            call()  # an eager call between replays
+            ops.sync()
+        g.free()
+    finally:
+        ops.set_stream(None)
+        st.free()
+
+
 def test_decode_ragged_repeats_bit_for_bit(rng):
     # The batch's (sequence, split) items are claimed by whichever workgroup
     # is free; every item still writes its own partial, so repeated calls on
