@@ -103,8 +103,9 @@ constexpr uint32_t kMergeNarrowSplits = kMergeNarrow / kMergeCols * kMergeBatch;
 // Keys per slot per iteration: fewer when G is large, to bound registers.
 // Ragged batches (many shorter-lived workgroups, each paying its first rows'
 // latency) keep more rows in flight: 64 sequences, 1025..16385 keys, 731 ->
-// 712 us per call with 4 instead of 2; one 32769-key sequence is slower
-// with 4 (45.4 -> 47.2 us per fused call).
+// 712 us per call with 4 instead of 2 (on the persistent batch kernel: 2
+// 688 us, 4 667, 8 792); one 32769-key sequence is slower with 4 (45.4 ->
+// 47.2 us per fused call).
 #ifndef FLK_DECODE_BATCH
 #define FLK_DECODE_BATCH 1  // ragged batches of up to kBatchMaxSeqs: persistent decode_batch_kernel
 #endif
