@@ -147,7 +147,9 @@ def test_workspace_bytes_covers_every_call_in_range():
     for H, Hkv in [(16, 8), (16, 16), (4, 1), (12, 4)]:
         for maxk, maxp in [(2048, 512), (32832, 64), (4096, 2048), (100, 100), (40000, 2048)]:
             ws = L.flk_workspace_bytes(H, Hkv, 128, maxk, maxp, 1)
-            for n in sorted({1, 2, 63, 64, 65, maxp // 2, maxp}):
+            # Around whole q tiles (64 rows / group queries) and their multiples.
+            for n in sorted({1, 2, 15, 16, 17, 20, 21, 22, 31, 32, 33, 41, 42, 43, 63, 64, 65,
+                             127, 128, 129, maxp // 2, maxp}):
                 for pos0 in sorted({0, 1, maxk // 3, maxk - 2 * n, maxk - n}):
                     if n < 1 or n > maxp or pos0 < 0 or pos0 + n > maxk:
                         continue
