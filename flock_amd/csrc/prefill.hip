@@ -54,6 +54,9 @@ constexpr int kHalfKB = 2;      // 16-key blocks per wave per tile
 constexpr uint32_t kMinPairedWG = 192;    // paired mode when it yields this many
 constexpr uint32_t kTargetSplitWG = 256;  // split mode aims at one workgroup per CU
 constexpr uint32_t kMinKtPerSplit = 2;
+#ifndef FLK_PREFILL_OPAD
+#define FLK_PREFILL_OPAD 4  // padding of the combine's o rows in LDS (floats)
+#endif
 #ifndef FLK_PREFILL_AHEAD
 #define FLK_PREFILL_AHEAD 1  // operand groups read from LDS ahead of their MFMAs
 #endif
@@ -382,10 +385,14 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   // their (m, l, acc) in the (now free) K tile buffer; the lower waves fold
   // them in and write the row.
   // Every wave has passed the last tile's barrier, so the K buffers are free.
+  // o rows padded to D + FLK_PREFILL_OPAD floats: the 16 lanes of a group
+  // hold 16 different rows, which then fall in distinct bank groups.
+  constexpr int LDO = D + FLK_PREFILL_OPAD;
+  static_assert(2 * kRows + kRows * LDO <= 2 * kBK * LDK, "combine data exceeds the K buffers");
   float* m_lds = k_lds;              // [kRows] m, then [kRows] l
-  float* o_lds = k_lds + 2 * kRows;  // [kRows][D]
+  float* o_lds = k_lds + 2 * kRows;  // [kRows][LDO]
   if (half == 1) {
-    float* dst = o_lds + r * D + 4 * CB * lg;
+    float* dst = o_lds + r * LDO + 4 * CB * lg;
 #pragma unroll
     for (int j = 0; j < 4; j++)
 #pragma unroll
@@ -407,7 +414,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   const float w1 = __builtin_amdgcn_exp2f(m_run - M);
   const float w2 = __builtin_amdgcn_exp2f(m2 - M);
   const float L = l_run * w1 + l2 * w2;
-  const float* o2 = o_lds + r * D + 4 * CB * lg;
+  const float* o2 = o_lds + r * LDO + 4 * CB * lg;
   float* dst;
   if (final) {
     if (!row_ok) return;
