@@ -600,6 +600,7 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_batch_kernel(DecodeArgs
     s_item = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
   __syncthreads();
   uint32_t it = s_item;
+  __syncthreads();  // every thread has read s_item before the first item writes it
   bool pre = false;  // ka, va and qld hold item it's first block and q
   float4 ka[U], va[U], kn[U], vn[U];
   float4 qld[QLD];

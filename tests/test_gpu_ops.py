@@ -192,10 +192,12 @@ def test_decode_parity_bar_long_context(rng, d, nk):
 
 @pytest.mark.parametrize("d", [128, 64])
 @pytest.mark.parametrize("H,Hkv,nk", [(12, 4, 700), (24, 4, 1500), (16, 2, 2049), (8, 1, 513),
-                                      (32, 4, 300), (6, 2, 4097)])
+                                      (32, 4, 300), (6, 2, 4097), (10, 2, 777), (14, 2, 1000),
+                                      (7, 1, 3000)])
 def test_decode_group_sizes(rng, d, H, Hkv, nk):
-    # GQA groups 3, 6, 8 and 8 with one kv head per workgroup (KH = 1, 2, 4):
-    # the template cases Qwen3's 16 / 8 layout never reaches, with key splits.
+    # GQA groups 3, 6, 8, 5 and 7, with one kv head per workgroup (KH = 1, 2,
+    # 4): the template cases Qwen3's 16 / 8 layout never reaches, with key
+    # splits.
     q = randn(rng, H * d)
     k, v = randn(rng, nk * Hkv * d), randn(rng, nk * Hkv * d)
     got = _decode(q, k, v, H, Hkv, d, nk)
@@ -365,6 +367,24 @@ def test_prefill_reference_cases(rng, H, Hkv, nq, pos0):
 def test_prefill_split_and_shapes(rng, d, H, Hkv, nq, pos0):
     # Long caches exercise the key-split + merge; odd groups exercise the
     # row -> (query, head) map (group 3 leaves rows 126, 127 of a tile unused).
+    nk = pos0 + nq
+    q = randn(rng, nq * H * d)
+    k, v = randn(rng, nk * Hkv * d), randn(rng, nk * Hkv * d)
+    got = _prefill(q, k, v, H, Hkv, d, nq, pos0)
+    want = oracle.attn_prefill(q, k, v, H, Hkv, d, nq, pos0)
+    m = metrics(got, want, cf.attention(q, k, v, H, Hkv, d, nq, pos0))
+    print(fmt(m))
+    assert meets_bar(m), fmt(m)
+
+
+@pytest.mark.parametrize("d", [128, 64])
+@pytest.mark.parametrize("H,Hkv,nq,pos0", [
+    (10, 2, 40, 3000), (12, 2, 45, 700), (14, 2, 30, 5000),  # split plans
+    (40, 8, 600, 0), (48, 8, 600, 0), (56, 8, 600, 0),        # paired plans
+])
+def test_prefill_groups_5_6_7(rng, d, H, Hkv, nq, pos0):
+    # 64 rows / G is 12, 10 and 9 queries: the last 4, 4 and 1 rows of every
+    # q tile have no query; the paired cases have >= 192 balanced pairs.
     nk = pos0 + nq
     q = randn(rng, nq * H * d)
     k, v = randn(rng, nk * Hkv * d), randn(rng, nk * Hkv * d)
