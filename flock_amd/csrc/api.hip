@@ -477,6 +477,11 @@ int32_t flk_attn_decode_ragged(const float* q, const float* kcache, const float*
   FLK_ALIGNED(kcache);
   FLK_ALIGNED(vcache);
   FLK_ALIGNED(o);
+  // The kernels read seq_row_off[b] and n_keys[b] as naturally aligned words.
+  if (reinterpret_cast<uintptr_t>(seq_row_off) % alignof(uint64_t) != 0 ||
+      reinterpret_cast<uintptr_t>(n_keys) % alignof(uint32_t) != 0)
+    return fail(FLK_ERR_ARG,
+                "ragged decode: seq_row_off must be 8-byte aligned and n_keys 4-byte aligned");
   int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
   if (rc) return rc;
   if (n_seqs == 0 || max_n_keys == 0)

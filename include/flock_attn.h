@@ -197,8 +197,10 @@ int32_t flk_decode_layer_noalloc(const float* q_raw, const float* k_raw, const f
  * call. q, o: [n_seqs][n_heads][head_dim]. Sequence b's cache rows start at
  * row seq_row_off[b] of kcache/vcache (rows of n_kv_heads*head_dim floats) and
  * it attends n_keys[b] keys (0: its o rows are zeros). seq_row_off and n_keys
- * are DEVICE arrays; max_n_keys bounds every n_keys[b] (larger values are
- * clamped to it). Up to 2048 sequences run on persistent workgroups that take
+ * are DEVICE arrays (8- and 4-byte aligned), so the library cannot check
+ * their contents: rows seq_row_off[b] .. seq_row_off[b] + n_keys[b] - 1 must
+ * lie inside kcache and vcache. max_n_keys bounds every n_keys[b] (larger
+ * values are clamped to it). Up to 2048 sequences run on persistent workgroups that take
  * the batch's (sequence, split) pieces from a counter kept in the workspace
  * (reset by the call itself); results are the same bits on every call. */
 int32_t flk_attn_decode_ragged(const float* q, const float* kcache, const float* vcache,

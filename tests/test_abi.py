@@ -233,6 +233,16 @@ def test_decode_layer_rejects_misaligned_raw_rows(which):
     assert rc == _lib.FLK_ERR_ARG and which in msg and "aligned" in msg
 
 
+@pytest.mark.parametrize("offs_off,nk_off", [(4, 0), (0, 2)])
+def test_ragged_rejects_misaligned_device_arrays(offs_off, nk_off):
+    # seq_row_off and n_keys are read as naturally aligned words on the device.
+    L = _lib.lib()
+    rc, msg = code_and_msg(L.flk_attn_decode_ragged(FAKE, FAKE, FAKE, FAKE + offs_off,
+                                                    FAKE + nk_off, FAKE, 4, 100, 16, 8, 128,
+                                                    FAKE, 1 << 30))
+    assert rc == _lib.FLK_ERR_ARG and "aligned" in msg
+
+
 def test_dropped_buffers_are_freed_at_sync_not_on_collection():
     # A DeviceBuffer that is garbage-collected must not call flk_free (which
     # waits for the device) on the spot; its pointer is parked until sync().
