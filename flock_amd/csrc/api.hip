@@ -456,6 +456,8 @@ int32_t flk_decode_layer_dev(const float* q_raw, const float* k_raw, const float
                              uint32_t n_kv_heads, uint32_t head_dim, uint32_t max_keys, void* ws,
                              uint64_t ws_bytes) {
   FLK_NONNULL(n_keys_dev);
+  if (reinterpret_cast<uintptr_t>(n_keys_dev) % alignof(uint32_t) != 0)
+    return fail(FLK_ERR_ARG, "decode_layer_dev: n_keys_dev must be 4-byte aligned");
   if (max_keys == 0) return fail(FLK_ERR_ARG, "decode_layer_dev max_keys 0");
   return decode_layer_common(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
                              vcache, o, max_keys, n_keys_dev, n_heads, n_kv_heads, head_dim, ws,

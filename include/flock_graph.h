@@ -20,8 +20,8 @@
 extern "C" {
 #endif
 
-/* flk_decode_layer with the key count in device memory: *n_keys_dev = pos + 1,
- * 1 <= *n_keys_dev <= max_keys. The launch shape depends only on max_keys, so
+/* flk_decode_layer with the key count in device memory (a 4-byte aligned
+ * word): *n_keys_dev = pos + 1, 1 <= *n_keys_dev <= max_keys. The launch shape depends only on max_keys, so
  * the call can be captured once and replayed at every position. ws:
  * flk_workspace_bytes(..., max_keys, 0, 1). The host cannot see the value, so
  * the kernel checks it: 0 or a value above max_keys (a cache that is full,

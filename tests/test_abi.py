@@ -243,6 +243,13 @@ def test_ragged_rejects_misaligned_device_arrays(offs_off, nk_off):
     assert rc == _lib.FLK_ERR_ARG and "aligned" in msg
 
 
+def test_decode_layer_dev_rejects_misaligned_key_count():
+    L = _lib.lib()
+    rc, msg = code_and_msg(L.flk_decode_layer_dev(*([FAKE] * 6), 1e-6, 0, *([FAKE] * 4),
+                                                  FAKE + 2, 16, 8, 128, 2048, FAKE, 1 << 30))
+    assert rc == _lib.FLK_ERR_ARG and "aligned" in msg
+
+
 def test_dropped_buffers_are_freed_at_sync_not_on_collection():
     # A DeviceBuffer that is garbage-collected must not call flk_free (which
     # waits for the device) on the spot; its pointer is parked until sync().
