@@ -13,8 +13,10 @@ of the hot path over one batch of synthetic, HBM-resident input:
   prefill2k  Causal prefill of 2048 tokens at position 0: fused prologue
              (norm + RoPE + K/V write), then MFMA flash attention.
              value = causal attention flops / step time (TFLOP/s).
-  ragged     64 independent sequences, n_keys ~ U[1025, 16385] (seeded),
-             ragged decode attention in one call. value in GB/s.
+  ragged     64 independent sequences, n_keys ~ U[1025, 16385] (seeded), one
+             decode step for all of them in one flk_decode_layer_ragged call:
+             per sequence q/k RMSNorm + RoPE at position n_keys - 1, the K/V
+             append, and attention. value in GB/s.
   chunk32k   A 64-token chunk at position 32768 onto a 32768-key cache, 28
              layers: prologue + chunked prefill attention. value in TFLOP/s.
   decode512  The same 28-layer step at 513 keys (4.2 MB per layer: it fits in
@@ -51,12 +53,17 @@ greedy generation at 32k context ("generate") and the 2048-token prompt
 ("prompt"). Inputs are N(0, 1) from a seeded generator (gains N(1, 0.1));
 caches are written on the device before timing starts.
 
-CPU baselines (after every GPU measurement): the oracle (oracle/, C) on a
-bounded sample of the same workload, 1 thread (value, cores 1) and OpenMP on
-the host's share of cores ("openmp"), with the host's CPU model and nproc.
-Decode at 32k runs the whole 28-layer step once on 1 thread; prefill2k and
-ragged run in full; chunk32k runs one of its 28 layers and states the x28
-extrapolation.
+CPU leg (after every GPU measurement). After a workload's timed region its
+inputs and outputs for one layer (the whole batch for ragged) are copied to
+the host; the oracle (oracle/, C) then runs on exactly those values. That run
+is both the CPU baseline -- 1 thread (value, cores 1) and OpenMP on the host's
+share of cores ("openmp"), with the host's CPU model and nproc -- and the
+parity check: "parity" holds max_abs and relErr of the GPU against the
+oracle, both distances from the float64 closed form, the clause of the bar
+that decided, the per-row argmax agreement, and bit-exactness of qn and the
+appended cache rows. Decode at 32k runs its layer 28 times on 1 thread (one
+whole step); prefill2k and ragged run in full; chunk32k runs one of its 28
+layers and states the x28 extrapolation.
 
 Timing: HIP events recorded on the stream the kernels are launched on bracket
 the K timed steps (after a synchronize). The roofline's average call duration
@@ -148,22 +155,35 @@ class Workload:
                            "the fp32 vector peak")
         return out
 
-    # CPU baseline: cpu_sample(threads) runs a bounded sample of the same
-    # workload through the oracle and returns (work done, seconds, what ran).
+    # CPU leg: capture() keeps host copies of the timed inputs and the GPU's
+    # outputs (self.host); cpu_sample(threads) runs the oracle on them and
+    # returns (work done, seconds, what ran), keeping the oracle's outputs of
+    # its first run in self.ref; parity() compares the two.
     cpu_sample = None
     cpu_parallel = True
+    host = None
+    ref = None
 
-    def cpu_baseline(self):
-        """The oracle on this host's cores: 1 thread (the primary figure, as the
-        reference's single-threaded TypeScript oracle), then OpenMP on the
-        host's share of cores."""
+    def capture(self):
+        pass
+
+    def parity(self):
+        return None
+
+    def cpu_leg(self, baseline=True):
+        """The oracle on this host's cores over the captured inputs: the CPU
+        baseline -- 1 thread (the primary figure, as the reference's
+        single-threaded TypeScript oracle), then OpenMP on the host's share
+        of cores -- and the parity of the GPU's outputs against it. Returns
+        (cpu_baseline or None, parity or None)."""
         if self.cpu_sample is None:
-            return None
+            return None, None
         import oracle
         model, nproc, share = cpu_info()
         scale = 1e9 if self.unit == "GB/s" else 1e12
         out = None
-        for th in (1, share):
+        legs = (1, share) if baseline else (share,)
+        for th in legs:
             oracle.set_threads(th)
             work, dt, what = self.cpu_sample(th)
             entry = {"value": round(work / dt / scale, 6), "unit": self.unit, "cores": th,
@@ -174,8 +194,28 @@ class Workload:
                 out["openmp"] = entry
             if share == 1 or not self.cpu_parallel:
                 break
+        oracle.set_threads(share)
+        par = self.parity()
         oracle.set_threads(1)
-        return out
+        return (out if baseline else None), par
+
+
+def host(x):
+    """A device tensor's values as a host numpy array (ordered after the work
+    queued on the current stream)."""
+    return x.detach().cpu().numpy().copy()
+
+
+def parity_entry(m, ids, inputs, **extra):
+    """The parity object of one workload: the bar's numbers (oracle/parity.py)."""
+    from oracle.parity import clause
+    out = {k: float(f"{m[k]:.3e}") for k in ("max_abs", "rel", "gpu_abs_vs_f64",
+                                               "oracle_abs_vs_f64") if k in m}
+    out["clause"] = clause(m)
+    out.update(ids)
+    out.update(extra)
+    out["inputs"] = inputs
+    return out
 
 
 def cpu_info():
@@ -253,28 +293,53 @@ class Decode32k(Workload):
                 "layers": self.L, "n_keys": self.nk, "n_heads": H, "n_kv_heads": HKV,
                 "head_dim": D, "batch": 1, "kv_cache_bytes": 2 * self.L * self.maxk * HKV * D * 4}
 
+    def capture(self, l=0):
+        """Layer l's timed inputs and the GPU's outputs, on the host."""
+        self.torch.cuda.synchronize()
+        h = {k: host(getattr(self, k)[l]) for k in ("q", "k", "v", "gq", "gk", "kc", "vc", "qn",
+                                                      "o")}
+        h["inv"] = host(self.inv)
+        row = HKV * D
+        p = self.pos * row
+        h["k_row"], h["v_row"] = h["kc"][p:p + row].copy(), h["vc"][p:p + row].copy()
+        self.host = h
+
     def cpu_sample(self, threads):
-        """oracle layer_attn_decode (norm, RoPE, append, attention) of whole
-        layers: 1 thread, one layer per layer of the step (the full step, on
-        one host cache); more threads, repeated for >= 3 s."""
+        """oracle layer_attn_decode (norm, RoPE, append, attention) of layer 0
+        of the timed step, on its inputs: 1 thread, once per layer of the step
+        (the full step's work); more threads, repeated for >= 3 s."""
         import oracle
-        rng = np.random.default_rng(5)
+        h = self.host
+        layer = lambda: oracle.layer_attn_decode(h["q"], h["k"], h["v"], h["gq"], h["gk"], h["inv"],
+                                                 h["kc"], h["vc"], self.pos, H, HKV, D)
+        first = layer()  # also the warm-up (pages the cache in)
+        if self.ref is None:
+            self.ref = first
         nk = self.nk
-        kc = rng.standard_normal(nk * HKV * D, dtype=np.float32)
-        vc = rng.standard_normal(nk * HKV * D, dtype=np.float32)
-        q, k, v = (rng.standard_normal(n, dtype=np.float32) for n in (H * D, HKV * D, HKV * D))
-        gq = rng.normal(1, 0.1, D).astype(np.float32)
-        gk = rng.normal(1, 0.1, D).astype(np.float32)
-        inv = oracle.rope_inv_freq(D)
-        layer = lambda: oracle.layer_attn_decode(q, k, v, gq, gk, inv, kc, vc, nk - 1, H, HKV, D)
-        layer()  # warm-up (page in the cache)
         if threads == 1 and self.L > 1:
             n, dt = timed(layer, 0.0, reps=self.L)
-            what = f"oracle layer_attn_decode x {n} layers (one whole step) over {nk} keys"
+            what = (f"oracle layer_attn_decode x {n} (one whole step's work) over {nk} keys, on "
+                    "the timed step's layer-0 inputs")
         else:
             n, dt = timed(layer, 3.0)
-            what = f"oracle layer_attn_decode x {n} over {nk} keys"
+            what = f"oracle layer_attn_decode x {n} over {nk} keys, on the timed layer-0 inputs"
         return n * self.work_per_call, dt, what
+
+    def parity(self):
+        from oracle import closed_form as cf
+        from oracle.parity import ids_check, metrics, projection_ids
+        h = self.host
+        qn, o = self.ref
+        m = metrics(h["o"], o, cf.attention(qn, h["kc"], h["vc"], H, HKV, D, 1, self.pos))
+        row, p = HKV * D, self.pos * HKV * D
+        return parity_entry(
+            m, ids_check(h["o"], o, H, m["max_abs"]),
+            "layer 0 of the timed step: its q/k/v, gains, cache and the GPU's qn, o and "
+            "appended row, copied to the host after the timed region",
+            projection_id_equal=projection_ids(h["o"])[0] == projection_ids(o)[0],
+            qn_bit_exact=bool(np.array_equal(h["qn"], qn)),
+            appended_row_bit_exact=bool(np.array_equal(h["k_row"], h["kc"][p:p + row]) and
+                                        np.array_equal(h["v_row"], h["vc"][p:p + row])))
 
 
 class Decode512(Decode32k):
@@ -352,29 +417,56 @@ class Prefill2k(Workload):
                 "layers": self.L, "n_queries": self.n, "pos0": self.pos0, "n_heads": H,
                 "n_kv_heads": HKV, "head_dim": D}
 
+    def capture(self, l=0):
+        """Layer l's timed inputs and the GPU's outputs, on the host."""
+        self.torch.cuda.synchronize()
+        h = {k: host(getattr(self, k)[l]) for k in ("q", "k", "v", "gq", "gk", "kc", "vc", "qn",
+                                                      "o")}
+        h["inv"] = host(self.inv)
+        p = self.pos0 * HKV * D
+        h["k_rows"], h["v_rows"] = h["kc"][p:].copy(), h["vc"][p:].copy()
+        self.host = h
+
     def cpu_sample(self, threads):
         """oracle layer_attn_prefill (norm, RoPE, append, causal attention) of
-        one layer at the workload's full size, once; more threads, repeated
+        layer 0 of the timed step, on its inputs, once; more threads, repeated
         for >= 2 s."""
         import oracle
-        rng = np.random.default_rng(6)
+        h = self.host
         n, pos0 = self.n, self.pos0
-        nk = pos0 + n
-        kc = np.zeros(nk * HKV * D, np.float32)
-        vc = np.zeros_like(kc)
-        kc[:pos0 * HKV * D] = rng.standard_normal(pos0 * HKV * D, dtype=np.float32)
-        vc[:pos0 * HKV * D] = rng.standard_normal(pos0 * HKV * D, dtype=np.float32)
-        q, k, v = (rng.standard_normal(n * w, dtype=np.float32) for w in (H * D, HKV * D, HKV * D))
-        gq = rng.normal(1, 0.1, D).astype(np.float32)
-        gk = rng.normal(1, 0.1, D).astype(np.float32)
-        inv = oracle.rope_inv_freq(D)
-        layer = lambda: oracle.layer_attn_prefill(q, k, v, gq, gk, inv, kc, vc, n, pos0, H, HKV, D)
-        reps, dt = timed(layer, 0.0 if threads == 1 else 2.0)
-        what = (f"oracle layer_attn_prefill x {reps}: {n} tokens at position {pos0}, one layer "
-                f"of {self.L}")
+        layer = lambda: oracle.layer_attn_prefill(h["q"], h["k"], h["v"], h["gq"], h["gk"],
+                                                  h["inv"], h["kc"], h["vc"], n, pos0, H, HKV, D)
+        reps, dt = 0, 0.0
+        if self.ref is None:  # the first run is timed too: same work every time
+            t0 = time.perf_counter()
+            self.ref = layer()
+            reps, dt = 1, time.perf_counter() - t0
+        if threads != 1 or reps == 0:
+            r2, dt2 = timed(layer, 0.0 if threads == 1 else 2.0)
+            reps, dt = r2, dt2
+        what = (f"oracle layer_attn_prefill x {reps}: {n} tokens at position {pos0}, layer 0 "
+                f"of {self.L} of the timed step")
         if self.L > 1:
             what += f" (the {self.L}-layer step extrapolates to {dt / reps * self.L:.1f} s)"
         return reps * self.work_per_call, dt, what
+
+    def parity(self):
+        from oracle import closed_form as cf
+        from oracle.parity import ids_check, metrics, projection_ids
+        h = self.host
+        qn, o = self.ref
+        n, pos0 = self.n, self.pos0
+        m = metrics(h["o"], o, cf.attention(qn, h["kc"], h["vc"], H, HKV, D, n, pos0))
+        p = pos0 * HKV * D
+        last = H * D  # the last token's output, what an LM head reads
+        return parity_entry(
+            m, ids_check(h["o"], o, n * H, m["max_abs"]),
+            "layer 0 of the timed step: its q/k/v, gains, cache and the GPU's qn, o and "
+            "appended rows, copied to the host after the timed region",
+            projection_id_equal=projection_ids(h["o"][-last:])[0] == projection_ids(o[-last:])[0],
+            qn_bit_exact=bool(np.array_equal(h["qn"], qn)),
+            appended_rows_bit_exact=bool(np.array_equal(h["k_rows"], h["kc"][p:]) and
+                                         np.array_equal(h["v_rows"], h["vc"][p:])))
 
 
 class Chunk32k(Prefill2k):
@@ -396,8 +488,9 @@ class Chunk32k(Prefill2k):
 
 class Ragged(Workload):
     name = "ragged"
-    kernel = ("flk_attn_decode_ragged: queue_zero_kernel + decode_batch_kernel<128,2,8> "
-              "(persistent, claimed items) + decode_merge_kernel<128>")
+    kernel = ("flk_decode_layer_ragged: qk_prologue_kernel<128,true> (norm + RoPE + append per "
+              "sequence; resets the item counters) + decode_batch_kernel<128,2,8> (persistent, "
+              "claimed items) + decode_merge_kernel<128,64>")
 
     def __init__(self, torch, ops, n_seqs=64, seed=3):
         self.torch, self.ops = torch, ops
@@ -408,47 +501,109 @@ class Ragged(Workload):
         self.rows = rows = int(self.n_keys.astype(np.uint64).sum())
         log(f"[ragged] {n_seqs} sequences, {rows} cache rows "
             f"({2 * rows * HKV * D * 4 / 1e9:.2f} GB)")
-        (self.kc, self.vc, self.q), _ = rng_inputs(torch, 77, [rows * HKV * D, rows * HKV * D,
-                                                                n_seqs * H * D])
+        (self.kc, self.vc, self.q, self.k, self.v), g = rng_inputs(
+            torch, 77, [rows * HKV * D, rows * HKV * D, n_seqs * H * D, n_seqs * HKV * D,
+                        n_seqs * HKV * D])
+        self.gq = 1 + 0.1 * torch.randn(D, device="cuda", generator=g)
+        self.gk = 1 + 0.1 * torch.randn(D, device="cuda", generator=g)
+        self.inv = torch.tensor(ops.rope_inv_freq(D, 1e6), device="cuda")
+        self.qn = torch.empty(n_seqs * H * D, device="cuda")
         self.o = torch.empty(n_seqs * H * D, device="cuda")
+        self.offs_h = offs.astype(np.uint64)
         self.offs = torch.tensor(offs.astype(np.int64), device="cuda")
         self.nkd = torch.tensor(self.n_keys.astype(np.int32), device="cuda")
         self.B, self.maxn = n_seqs, int(self.n_keys.max())
         self.ws = ops.Workspace(H, HKV, D, self.maxn, 0, n_seqs)
-        self.work_per_call = 2 * rows * HKV * D * 4 + 2 * n_seqs * H * D * 4
+        # Algorithmic bytes: every K and V row once (the new one written), and
+        # per sequence raw q, k, v in and o out.
+        self.work_per_call = (2 * rows * HKV * D * 4
+                              + n_seqs * (2 * H * D * 4 + 2 * HKV * D * 4))
         self.work_per_step = self.work_per_call
 
     def call(self, l=0):
-        self.ops.attn_decode_ragged(self.q, self.kc, self.vc, self.offs, self.nkd, self.o, self.B,
-                                    self.maxn, H, HKV, D, self.ws)
+        self.ops.decode_layer_ragged(self.q, self.k, self.v, self.gq, self.gk, self.inv, EPS,
+                                     "neox", self.qn, self.kc, self.vc, self.offs, self.nkd,
+                                     self.o, self.B, self.maxn, H, HKV, D, self.ws)
 
     def step(self):
         self.call()
 
     def config(self):
-        return {"workload": f"ragged GQA decode, {self.B} sequences, n_keys U[1025,16385] "
-                            f"(sum {self.rows})", "n_seqs": self.B, "sum_n_keys": self.rows,
-                "n_heads": H, "n_kv_heads": HKV, "head_dim": D}
+        return {"workload": f"ragged GQA decode step, {self.B} sequences, n_keys U[1025,16385] "
+                            f"(sum {self.rows}): per sequence q/k RMSNorm + RoPE at position "
+                            "n_keys - 1 + K/V append + split-K attention, one call",
+                "n_seqs": self.B, "sum_n_keys": self.rows, "n_heads": H, "n_kv_heads": HKV,
+                "head_dim": D}
+
+    def capture(self):
+        self.torch.cuda.synchronize()
+        h = {k: host(getattr(self, k)) for k in ("q", "k", "v", "gq", "gk", "inv", "kc", "vc",
+                                                  "qn", "o")}
+        row = HKV * D
+        last = [(int(self.offs_h[b]) + int(self.n_keys[b]) - 1) * row for b in range(self.B)]
+        h["k_rows"] = np.stack([h["kc"][p:p + row] for p in last])
+        h["v_rows"] = np.stack([h["vc"][p:p + row] for p in last])
+        self.host = h
+
+    def _seq(self, b):
+        h, row = self.host, HKV * D
+        s, n = int(self.offs_h[b]) * row, int(self.n_keys[b])
+        return (h["q"][b * H * D:(b + 1) * H * D], h["k"][b * row:(b + 1) * row],
+                h["v"][b * row:(b + 1) * row], h["kc"][s:s + n * row], h["vc"][s:s + n * row], n)
 
     def cpu_sample(self, threads):
-        """oracle attn over every sequence of the batch in order (one host cache
-        of the longest length, sliced per sequence); more threads, the batch
-        repeated for >= 2 s."""
+        """oracle layer_attn_decode (norm, RoPE, append, attention) of every
+        sequence of the timed batch in order, on its inputs; more threads, the
+        batch repeated for >= 2 s."""
         import oracle
-        rng = np.random.default_rng(8)
-        longest = int(self.n_keys.max())
-        kc = rng.standard_normal(longest * HKV * D, dtype=np.float32)
-        vc = rng.standard_normal(longest * HKV * D, dtype=np.float32)
-        q = rng.standard_normal(H * D, dtype=np.float32)
+        h = self.host
 
         def batch():
-            for nk in self.n_keys:
-                nk = int(nk)
-                oracle.attn(q, kc[:nk * HKV * D], vc[:nk * HKV * D], H, HKV, D, nk)
+            outs = []
+            for b in range(self.B):
+                q, k, v, kc, vc, n = self._seq(b)  # cache views: appended in place
+                outs.append(oracle.layer_attn_decode(q, k, v, h["gq"], h["gk"], h["inv"], kc, vc,
+                                                     n - 1, H, HKV, D))
+            return outs
 
-        reps, dt = timed(batch, 0.0 if threads == 1 else 2.0)
-        return reps * self.work_per_call, dt, (f"oracle attn over all {self.B} sequences "
-                                               f"({self.rows} keys) x {reps}")
+        reps, dt = 0, 0.0
+        if self.ref is None:
+            t0 = time.perf_counter()
+            self.ref = batch()
+            reps, dt = 1, time.perf_counter() - t0
+        if threads != 1 or reps == 0:
+            reps, dt = timed(batch, 0.0 if threads == 1 else 2.0)
+        return reps * self.work_per_call, dt, (
+            f"oracle layer_attn_decode over all {self.B} sequences of the timed batch "
+            f"({self.rows} keys) x {reps}")
+
+    def parity(self):
+        from oracle import closed_form as cf
+        from oracle.parity import clause, ids_check, metrics
+        h, row = self.host, HKV * D
+        worst, clauses, ids_ok, ties, qn_ok, rows_ok = None, {}, True, 0, True, True
+        for b in range(self.B):
+            q, k, v, kc, vc, n = self._seq(b)
+            qn, o = self.ref[b]
+            got = h["o"][b * H * D:(b + 1) * H * D]
+            m = metrics(got, o, cf.attention(qn, kc, vc, H, HKV, D, 1, n - 1))
+            c = clause(m)
+            clauses[c] = clauses.get(c, 0) + 1
+            ids = ids_check(got, o, H, m["max_abs"])
+            ids_ok &= ids["argmax_equal"]
+            ties += ids["near_tie_rows"]
+            qn_ok &= bool(np.array_equal(h["qn"][b * H * D:(b + 1) * H * D], qn))
+            rows_ok &= bool(np.array_equal(h["k_rows"][b], kc[(n - 1) * row:]) and
+                            np.array_equal(h["v_rows"][b], vc[(n - 1) * row:]))
+            if worst is None or m["rel"] > worst[1]["rel"]:
+                worst = (b, m)
+        return parity_entry(
+            worst[1], {"argmax_equal": ids_ok, "argmax_rows": self.B * H, "near_tie_rows": ties},
+            "every sequence of the timed batch: its q/k/v, gains, cache and the GPU's qn, o and "
+            "appended rows, copied to the host after the timed region; numbers of the sequence "
+            "with the largest relErr",
+            worst_seq=worst[0], worst_seq_n_keys=int(self.n_keys[worst[0]]),
+            clauses_over_sequences=clauses, qn_bit_exact=qn_ok, appended_rows_bit_exact=rows_ok)
 
 
 class Copy(Workload):
@@ -512,21 +667,37 @@ class Q8LmHead(Workload):
         return {"workload": f"Q8_0 matvec {self.rows} x {self.cols} (LM head), 1 token",
                 "rows": self.rows, "cols": self.cols, "weight_bytes": self.rows * self.cols * 34 // 32}
 
+    def capture(self):
+        """The weights, x and output of the last timed call, on the host."""
+        self.torch.cuda.synchronize()
+        c = (self.i - 1) % self.copies
+        blocks = np.empty((self.rows * self.cols // 32, 34), np.uint8)
+        blocks[:, :2] = host(self.sc[c]).view(np.uint8).reshape(-1, 2)
+        blocks[:, 2:] = host(self.qs[c]).view(np.uint8).reshape(-1, 32)
+        self.host = {"packed": blocks.ravel(), "x": host(self.x), "o": host(self.o)}
+
     def cpu_sample(self, threads):
-        """oracle.q8_matvec (coop(64); a serial loop, so 1 thread) on 4096-row
-        slices of the head for >= 5 s."""
+        """oracle.q8_matvec (coop(64); a serial loop, so 1 thread) of the whole
+        head on the last timed call's weights and x, for >= 5 s."""
         import oracle
-        rng = np.random.default_rng(9)
-        rows = 4096
-        blocks = np.empty((rows * self.cols // 32, 34), np.uint8)
-        blocks[:, :2] = (np.abs(rng.standard_normal(blocks.shape[0])) * 4e-4 + 1e-5).astype(
-            np.float16).view(np.uint8).reshape(-1, 2)
-        blocks[:, 2:] = rng.integers(0, 256, (blocks.shape[0], 32), dtype=np.uint8)
-        packed = blocks.ravel()
-        x = rng.standard_normal(self.cols).astype(np.float32)
-        n, dt = timed(lambda: oracle.q8_matvec(packed, x, rows, self.cols, 64), 5.0)
-        per = rows * self.cols * 34 // 32 + 4 * (self.cols + rows)
-        return n * per, dt, f"oracle q8_matvec of a {rows} x {self.cols} slice x {n}"
+        h = self.host
+        run = lambda: oracle.q8_matvec(h["packed"], h["x"], self.rows, self.cols, 64)
+        if self.ref is None:
+            self.ref = run()
+        n, dt = timed(run, 5.0)
+        return n * self.work_per_call, dt, (f"oracle q8_matvec of the whole {self.rows} x "
+                                            f"{self.cols} head (the last timed call's weights) "
+                                            f"x {n}")
+
+    def parity(self):
+        from oracle.parity import metrics
+        from oracle import argmax
+        h, want = self.host, self.ref
+        m = metrics(h["o"], want)
+        return parity_entry(
+            m, {"argmax_equal": argmax(h["o"]) == argmax(want)},
+            "the last timed call's weights, x and output, copied to the host after the timed "
+            "region", bit_exact=bool(np.array_equal(h["o"], want)))
 
     cpu_parallel = False  # the q8 oracle has no parallel loop
 
@@ -973,7 +1144,8 @@ def run(torch, ops, stream, name, steps, warmup):
            "roofline": w.roofline(call_ms, traffic_from_profiles(f"{name}_pmc.md"))}
     if hasattr(w, "extra"):
         out.update(w.extra(ms, call_ms))
-    # Drop the device buffers; the CPU baseline needs only the sizes.
+    w.capture()  # host copies of the timed inputs and outputs for the CPU leg
+    # Drop the device buffers; the CPU leg needs only the host copies.
     if getattr(w, "graph", None) is not None:
         w.graph.free()
         w.graph = None
@@ -985,7 +1157,7 @@ def run(torch, ops, stream, name, steps, warmup):
         delattr(w, k)
     ops.sync()  # also releases the dropped buffers
     torch.cuda.empty_cache()
-    return out, w.cpu_baseline
+    return out, w.cpu_leg
 
 
 def main():
@@ -994,7 +1166,10 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=3)
     ap.add_argument("--workload", default="decode32k", choices=sorted(WORKLOADS))
-    ap.add_argument("--no-cpu-baseline", action="store_true")
+    ap.add_argument("--no-cpu-baseline", action="store_true",
+                    help="skip the CPU baseline timing (the parity check still runs)")
+    ap.add_argument("--no-parity", action="store_true",
+                    help="skip the whole CPU leg: no CPU baseline and no parity check")
     ap.add_argument("--no-secondary", action="store_true",
                     help="measure only the main workload (the default run also measures "
                          "prefill2k, decode512, ragged, chunk32k, q8lmhead, gen32k, prompt2k)")
@@ -1054,15 +1229,21 @@ def main():
                     res["frac_of_fp32_mfma_peak"] = round(res["value"] / FP32_MFMA_PEAK_TFLOPS, 4)
                 out[key] = res
                 secondary.append((key, name, cpu))
-    # CPU baselines last, with the GPU measurements done.
-    if not args.no_cpu_baseline:
-        log(f"[{args.workload}] CPU baseline (oracle port)")
-        out["cpu_baseline"] = main_cpu()
-        for key, name, cpu in secondary:
-            log(f"[{name}] CPU baseline (oracle port)")
-            cb = cpu()
+    # The CPU leg last, with the GPU measurements done: the oracle on the
+    # timed inputs, as the CPU baseline and as the parity check.
+    if not args.no_parity:
+        baseline = not args.no_cpu_baseline
+        for key, name, cpu in [(None, args.workload, main_cpu)] + secondary:
+            log(f"[{name}] CPU leg: oracle on the timed inputs"
+                f"{' (baseline + parity)' if baseline else ' (parity)'}")
+            cb, par = cpu(baseline)
+            dst = out if key is None else out[key]
             if cb is not None:
-                out[key]["cpu_baseline"] = cb
+                dst["cpu_baseline"] = cb
+            if par is not None:
+                dst["parity"] = par
+                log(f"[{name}] parity: {par['clause']}, max_abs {par.get('max_abs')}, "
+                    f"rel {par.get('rel')}")
     print(json.dumps(out), flush=True)
 
 

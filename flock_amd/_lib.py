@@ -67,6 +67,10 @@ SIGNATURES: dict[str, tuple] = {
     ),
     "flk_attn_decode_ragged": (
         _i32, [_p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32, _u32, _p, _u64]),
+    "flk_decode_layer_ragged": (
+        _i32,
+        [_p, _p, _p, _p, _p, _p, _f32, _i32, _p, _p, _p, _p, _p, _p, _u32, _u32, _u32, _u32,
+         _u32, _p, _u64]),
     # include/flock_q8.h
     "flk_q8_matvec": (_i32, [_p, _p, _p, _p, _u32, _u32, _u32]),
     "flk_q8_split": (_i32, [_p, _u32, _u32, _p, _p]),

@@ -464,38 +464,90 @@ int32_t flk_decode_layer_dev(const float* q_raw, const float* k_raw, const float
                              ws_bytes, "flk_decode_layer_dev");
 }
 
-int32_t flk_attn_decode_ragged(const float* q, const float* kcache, const float* vcache,
-                               const uint64_t* seq_row_off, const uint32_t* n_keys, float* o,
-                               uint32_t n_seqs, uint32_t max_n_keys, uint32_t n_heads,
-                               uint32_t n_kv_heads, uint32_t head_dim, void* ws,
-                               uint64_t ws_bytes) {
-  FLK_NONNULL(q);
+}  // extern "C"
+
+// Checks shared by the two ragged entry points (before any launch).
+static int32_t check_ragged(const float* kcache, const float* vcache, const uint64_t* seq_row_off,
+                            const uint32_t* n_keys, const float* o, uint32_t n_seqs,
+                            uint32_t max_n_keys, uint32_t n_heads, uint32_t n_kv_heads,
+                            uint32_t head_dim, void* ws, uint64_t ws_bytes, const char* what) {
   FLK_NONNULL(kcache);
   FLK_NONNULL(vcache);
   FLK_NONNULL(seq_row_off);
   FLK_NONNULL(n_keys);
   FLK_NONNULL(o);
-  FLK_ALIGNED(q);
   FLK_ALIGNED(kcache);
   FLK_ALIGNED(vcache);
   FLK_ALIGNED(o);
   // The kernels read seq_row_off[b] and n_keys[b] as naturally aligned words.
   if (reinterpret_cast<uintptr_t>(seq_row_off) % alignof(uint64_t) != 0 ||
       reinterpret_cast<uintptr_t>(n_keys) % alignof(uint32_t) != 0)
-    return fail(FLK_ERR_ARG,
-                "ragged decode: seq_row_off must be 8-byte aligned and n_keys 4-byte aligned");
+    return fail(FLK_ERR_ARG, "%s: seq_row_off must be 8-byte aligned and n_keys 4-byte aligned",
+                what);
   int32_t rc = check_heads(n_heads, n_kv_heads, head_dim);
   if (rc) return rc;
   if (n_seqs == 0 || max_n_keys == 0)
-    return fail(FLK_ERR_ARG, "ragged decode n_seqs=%u max_n_keys=%u", n_seqs, max_n_keys);
+    return fail(FLK_ERR_ARG, "%s n_seqs=%u max_n_keys=%u", what, n_seqs, max_n_keys);
   if (n_seqs > 65535)
-    return fail(FLK_ERR_UNSUPPORTED, "ragged decode n_seqs %u exceeds 65535 (grid z)", n_seqs);
+    return fail(FLK_ERR_UNSUPPORTED, "%s n_seqs %u exceeds 65535 (grid z)", what, n_seqs);
   const DecodeShape s{n_heads, n_kv_heads, head_dim, n_seqs, max_n_keys};
-  rc = check_ws(ws, ws_bytes, decode_ws_bytes(s));
+  return check_ws(ws, ws_bytes, decode_ws_bytes(s));
+}
+
+extern "C" {
+
+int32_t flk_attn_decode_ragged(const float* q, const float* kcache, const float* vcache,
+                               const uint64_t* seq_row_off, const uint32_t* n_keys, float* o,
+                               uint32_t n_seqs, uint32_t max_n_keys, uint32_t n_heads,
+                               uint32_t n_kv_heads, uint32_t head_dim, void* ws,
+                               uint64_t ws_bytes) {
+  FLK_NONNULL(q);
+  FLK_ALIGNED(q);
+  int32_t rc = check_ragged(kcache, vcache, seq_row_off, n_keys, o, n_seqs, max_n_keys, n_heads,
+                            n_kv_heads, head_dim, ws, ws_bytes, "ragged decode");
   if (rc) return rc;
+  const DecodeShape s{n_heads, n_kv_heads, head_dim, n_seqs, max_n_keys};
   return hip_status(
       launch_decode(q, kcache, vcache, o, seq_row_off, n_keys, s, nullptr, ws, g_stream),
       "flk_attn_decode_ragged");
+}
+
+int32_t flk_decode_layer_ragged(const float* q_raw, const float* k_raw, const float* v_raw,
+                                const float* gq, const float* gk, const float* inv_freq,
+                                float eps, int32_t pairing, float* qn_out, float* kcache,
+                                float* vcache, const uint64_t* seq_row_off,
+                                const uint32_t* n_keys, float* o, uint32_t n_seqs,
+                                uint32_t max_n_keys, uint32_t n_heads, uint32_t n_kv_heads,
+                                uint32_t head_dim, void* ws, uint64_t ws_bytes) {
+  FLK_NONNULL(q_raw);
+  FLK_NONNULL(k_raw);
+  FLK_NONNULL(v_raw);
+  FLK_NONNULL(gq);
+  FLK_NONNULL(gk);
+  FLK_NONNULL(inv_freq);
+  FLK_NONNULL(qn_out);
+  FLK_ALIGNED(qn_out);  // the attention launch reads qn as float4s
+  if (pairing != FLK_ROPE_NEOX && pairing != FLK_ROPE_NORM)
+    return fail(FLK_ERR_ARG, "rope pairing %d (0 = neox, 1 = norm)", pairing);
+  int32_t rc = check_ragged(kcache, vcache, seq_row_off, n_keys, o, n_seqs, max_n_keys, n_heads,
+                            n_kv_heads, head_dim, ws, ws_bytes, "ragged decode layer");
+  if (rc) return rc;
+  const DecodeShape s{n_heads, n_kv_heads, head_dim, n_seqs, max_n_keys};
+  DecodeFused f;
+  f.q_raw = q_raw;
+  f.k_raw = k_raw;
+  f.v_raw = v_raw;
+  f.gq = gq;
+  f.gk = gk;
+  f.inv_freq = inv_freq;
+  f.eps = eps;
+  f.pairing = pairing;
+  f.qn_out = qn_out;
+  f.kcache_w = kcache;
+  f.vcache_w = vcache;
+  return hip_status(
+      launch_decode(qn_out, kcache, vcache, o, seq_row_off, n_keys, s, &f, ws, g_stream),
+      "flk_decode_layer_ragged");
 }
 
 }  // extern "C"

@@ -258,6 +258,14 @@ struct DecodeShape {
   uint32_t max_n_keys;  // n_keys for a single sequence
 };
 
+// The ragged layer step's prologue: per sequence b, norm + RoPE of q and k at
+// position n_keys[b] - 1, qn_out rows and the append at row seq_row_off[b] +
+// n_keys[b] - 1; also zeroes n_queue counters at `queue` (when not null).
+hipError_t launch_ragged_prologue(const DecodeFused& f, const uint64_t* seq_row_off,
+                                  const uint32_t* n_keys, uint32_t n_seqs, uint32_t max_n_keys,
+                                  uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                                  uint32_t* queue, uint32_t n_queue, hipStream_t st);
+
 uint64_t decode_ws_bytes(const DecodeShape& s);
 uint64_t decode_ws_bound(const DecodeShape& s);
 hipError_t launch_decode(const float* q, const float* kcache, const float* vcache, float* o,

@@ -51,6 +51,7 @@ struct DecodeArgs {
   const uint64_t* seq_row_off;  // ragged only
   const uint32_t* n_keys_dev;   // ragged only
   uint32_t n_keys;              // single sequence (ragged: the bound max_n_keys)
+  uint32_t strict;              // ragged layer step: n_keys[b] > n_keys is refused (NaN rows)
   uint32_t n_heads, n_kv_heads;
   uint32_t kpi;                 // keys per block (one loop iteration of a slot group)
   uint32_t bps;                 // blocks per split (a sequence's split count divisor)
@@ -131,12 +132,22 @@ __device__ __forceinline__ uint32_t seq_splits(const DecodeArgs& a, uint32_t n_k
 // the key count in device memory (flk_decode_layer_dev) accepts only 1 ..
 // max_keys there: any other value gives 0, and the split kernel then fills o
 // with NaN and appends nothing (the reference throws "KV cache full" on the
-// host, layer.ts:575; a replayed graph has no host step to throw from).
+// host, layer.ts:575; a replayed graph has no host step to throw from). The
+// ragged layer step (strict) likewise refuses n_keys[b] > max_n_keys, whose
+// prologue appended nothing; its n_keys[b] == 0 is an idle sequence.
 __device__ __forceinline__ uint32_t seq_keys(const DecodeArgs& a, uint32_t seq) {
   if (a.n_keys_dev == nullptr) return a.n_keys;
   const uint32_t v = a.n_keys_dev[seq];
-  if (a.q_raw != nullptr) return v <= a.n_keys ? v : 0u;
+  if (a.q_raw != nullptr || a.strict) return v <= a.n_keys ? v : 0u;
   return min(v, a.n_keys);
+}
+
+// o rows of a sequence with no keys to attend: zeros for an empty (idle)
+// sequence, NaN for a key count the device refused.
+__device__ __forceinline__ float empty_fill(const DecodeArgs& a, uint32_t seq) {
+  if (a.q_raw != nullptr) return __builtin_nanf("");
+  if (a.strict && a.n_keys_dev[seq] != 0u) return __builtin_nanf("");
+  return 0.f;
 }
 
 // U keys of one slot: rows base + u * PH + ph. Past the end of the split the
@@ -308,9 +319,9 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_split_kernel(DecodeArgs
 
   const uint32_t n_keys = seq_keys(a, seq);
   const uint64_t row0 = a.seq_row_off != nullptr ? a.seq_row_off[seq] : 0;
-  if (n_keys == 0) {  // empty ragged sequence: zero rows; bad device position: NaN rows
+  if (n_keys == 0) {  // empty ragged sequence: zero rows; refused key count: NaN rows
     if (split == 0) {
-      const float fill = a.q_raw != nullptr ? __builtin_nanf("") : 0.f;
+      const float fill = empty_fill(a, seq);
       for (int i = tid; i < HG * D; i += kDecodeThreads)
         a.o[((size_t)seq * a.n_heads + h0) * D + i] = fill;
     }
@@ -611,9 +622,10 @@ __global__ __launch_bounds__(kDecodeThreads) void decode_batch_kernel(DecodeArgs
       claim = __hip_atomic_fetch_add(counter, 1u, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
     uint32_t seq, split, n_keys;
     locate(it, seq, split, n_keys);
-    if (n_keys == 0) {  // empty sequence: zero rows
+    if (n_keys == 0) {  // empty sequence: zero rows (refused key count: NaN)
+      const float fill = empty_fill(a, seq);
       for (int i = tid; i < HG * D; i += kDecodeThreads)
-        a.o[((size_t)seq * a.n_heads + h0) * D + i] = 0.f;
+        a.o[((size_t)seq * a.n_heads + h0) * D + i] = fill;
       if (tid == 0) s_item = claim;
       __syncthreads();
       it = s_item;
@@ -987,7 +999,15 @@ hipError_t launch_decode(const float* q, const float* kcache, const float* vcach
     a.part_ml = reinterpret_cast<float2*>(w);
     a.part_acc = reinterpret_cast<float*>(w + ws_align(slots * sizeof(float2)));
   }
-  if (fused != nullptr) {
+  // The ragged layer step: its prologue launch (norm + RoPE of every
+  // sequence's q and k, the append, and the batch kernel's counter reset)
+  // writes qn and the new cache rows, then the batch runs as plain ragged
+  // decode over qn, refusing key counts past the bound.
+  const bool ragged_layer = fused != nullptr && seq_row_off != nullptr;
+  if (ragged_layer) {
+    a.q = fused->qn_out;
+    a.strict = 1;
+  } else if (fused != nullptr) {
     a.q_raw = fused->q_raw;
     a.k_raw = fused->k_raw;
     a.v_raw = fused->v_raw;
@@ -1003,10 +1023,16 @@ hipError_t launch_decode(const float* q, const float* kcache, const float* vcach
   const dim3 grid(groups, a.max_splits, s.n_seqs);
   const uint32_t G = s.n_heads / s.n_kv_heads;
   hipError_t e;
+  if (ragged_layer) {
+    e = launch_ragged_prologue(*fused, seq_row_off, n_keys_dev, s.n_seqs, s.max_n_keys,
+                               s.n_heads, s.n_kv_heads, s.head_dim, queue, groups, st);
+    if (e != hipSuccess) return e;
+  }
   if (batch) {
     // The counters start at zero: a kernel, not a memset, so that a captured
-    // graph replays it.
-    hipLaunchKernelGGL(queue_zero_kernel, dim3(1), dim3(kBatchMaxGroups), 0, st, queue, groups);
+    // graph replays it (the ragged layer step's prologue zeroes them).
+    if (!ragged_layer)
+      hipLaunchKernelGGL(queue_zero_kernel, dim3(1), dim3(kBatchMaxGroups), 0, st, queue, groups);
     const dim3 bgrid(groups, kBatchWG / groups > 0 ? kBatchWG / groups : 1);
     e = s.head_dim == 128 ? launch_batch_d<128>(a, bgrid, G, KH, s.n_seqs, queue, st)
                           : launch_batch_d<64>(a, bgrid, G, KH, s.n_seqs, queue, st);

@@ -104,20 +104,50 @@ hipError_t launch_kv_append(const float* kn, const float* v, float* kcache, floa
 // -> kcache row pos0 + token), the last n_kv_heads are v heads (copied raw to
 // vcache). Identical arithmetic to rmsnorm_kernel + rope_kernel for head_dim
 // vectors, so the caches match the unfused path bit for bit.
+//
+// Ragged batches (RAGGED, flk_decode_layer_ragged): "token" b is sequence b's
+// new token. Its position is n_keys[b] - 1 and its cache row is seq_row_off[b]
+// + n_keys[b] - 1. A sequence with n_keys[b] == 0 is idle (its qn rows are
+// zeroed, nothing is appended); one with n_keys[b] > max_n_keys is refused on
+// the device (qn rows NaN, nothing appended: the attention launch after it
+// fills that sequence's o with NaN too). Workgroup 0 also zeroes the
+// n_queue item counters of the batch decode kernel that follows on the
+// stream, so the ragged step needs no separate reset launch.
 constexpr int kPrologueThreads = 256;
 
-template <int D>
+struct RaggedTokens {
+  const uint32_t* n_keys = nullptr;       // [n_seqs]
+  const uint64_t* seq_row_off = nullptr;  // [n_seqs]
+  uint32_t max_n_keys = 0;
+  uint32_t* queue = nullptr;              // item counters to zero (or null)
+  uint32_t n_queue = 0;
+};
+
+template <int D, bool RAGGED>
 __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
     const float* __restrict__ q_raw, const float* __restrict__ k_raw,
     const float* __restrict__ v_raw, const float* __restrict__ gq, const float* __restrict__ gk,
     const float* __restrict__ inv_freq, float eps, int32_t pairing, float* __restrict__ qn_out,
     float* __restrict__ kcache, float* __restrict__ vcache, uint32_t pos0, uint32_t n_heads,
-    uint32_t n_kv_heads, uint32_t q_stride, uint32_t kv_stride) {
+    uint32_t n_kv_heads, uint32_t q_stride, uint32_t kv_stride, RaggedTokens rt) {
   __shared__ float2 s_cs[D / 2];
   const int lane = threadIdx.x & 63;
   const int wave = threadIdx.x >> 6;
   const uint32_t tok = blockIdx.x;
-  const uint32_t pos = pos0 + tok;
+  uint32_t pos = pos0 + tok;
+  uint64_t cache_row = pos;
+  if constexpr (RAGGED) {
+    if (tok == 0 && threadIdx.x < rt.n_queue) rt.queue[threadIdx.x] = 0u;
+    const uint32_t nk = rt.n_keys[tok];
+    if (nk == 0 || nk > rt.max_n_keys) {  // idle (zeros) or refused (NaN): no append
+      const float fill = nk == 0 ? 0.f : __builtin_nanf("");
+      float* dq = qn_out + (size_t)tok * n_heads * D;
+      for (uint32_t i = threadIdx.x; i < n_heads * D; i += kPrologueThreads) dq[i] = fill;
+      return;  // uniform per workgroup
+    }
+    pos = nk - 1;
+    cache_row = rt.seq_row_off[tok] + pos;
+  }
   const uint32_t per_tok = n_heads + 2 * n_kv_heads;
   const size_t kv_row = (size_t)n_kv_heads * D;
   // Vector idx -> (source, destination, gain): q heads, then k heads, then v.
@@ -130,12 +160,12 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
     } else if (idx < n_heads + n_kv_heads) {
       const uint32_t h = idx - n_heads;
       src = k_raw + (size_t)tok * kv_stride + (size_t)h * D;
-      dst = kcache + (size_t)pos * kv_row + (size_t)h * D;
+      dst = kcache + cache_row * kv_row + (size_t)h * D;
       g = gk;
     } else {
       const uint32_t h = idx - n_heads - n_kv_heads;
       src = v_raw + (size_t)tok * kv_stride + (size_t)h * D;
-      dst = vcache + (size_t)pos * kv_row + (size_t)h * D;
+      dst = vcache + cache_row * kv_row + (size_t)h * D;
     }
   };
   // Each wave takes vectors wave, wave + 4, ...; a batch of kBatch vectors is
@@ -211,14 +241,39 @@ hipError_t launch_qk_prologue(const float* q_raw, const float* k_raw, const floa
   // Raw rows of consecutive tokens: packed, or in_stride floats apart.
   const uint32_t q_stride = in_stride ? in_stride : n_heads * head_dim;
   const uint32_t kv_stride = in_stride ? in_stride : n_kv_heads * head_dim;
+  const RaggedTokens none{};
   if (head_dim == 128)
-    hipLaunchKernelGGL(qk_prologue_kernel<128>, dim3(n_tokens), dim3(kPrologueThreads), 0, st,
-                       q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
-                       vcache, pos0, n_heads, n_kv_heads, q_stride, kv_stride);
+    hipLaunchKernelGGL((qk_prologue_kernel<128, false>), dim3(n_tokens), dim3(kPrologueThreads), 0,
+                       st, q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
+                       vcache, pos0, n_heads, n_kv_heads, q_stride, kv_stride, none);
   else
-    hipLaunchKernelGGL(qk_prologue_kernel<64>, dim3(n_tokens), dim3(kPrologueThreads), 0, st,
-                       q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
-                       vcache, pos0, n_heads, n_kv_heads, q_stride, kv_stride);
+    hipLaunchKernelGGL((qk_prologue_kernel<64, false>), dim3(n_tokens), dim3(kPrologueThreads), 0,
+                       st, q_raw, k_raw, v_raw, gq, gk, inv_freq, eps, pairing, qn_out, kcache,
+                       vcache, pos0, n_heads, n_kv_heads, q_stride, kv_stride, none);
+  return hipGetLastError();
+}
+
+hipError_t launch_ragged_prologue(const DecodeFused& f, const uint64_t* seq_row_off,
+                                  const uint32_t* n_keys, uint32_t n_seqs, uint32_t max_n_keys,
+                                  uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                                  uint32_t* queue, uint32_t n_queue, hipStream_t st) {
+  RaggedTokens rt;
+  rt.n_keys = n_keys;
+  rt.seq_row_off = seq_row_off;
+  rt.max_n_keys = max_n_keys;
+  rt.queue = queue;
+  rt.n_queue = queue != nullptr ? n_queue : 0;
+  const uint32_t q_stride = n_heads * head_dim, kv_stride = n_kv_heads * head_dim;
+  if (head_dim == 128)
+    hipLaunchKernelGGL((qk_prologue_kernel<128, true>), dim3(n_seqs), dim3(kPrologueThreads), 0,
+                       st, f.q_raw, f.k_raw, f.v_raw, f.gq, f.gk, f.inv_freq, f.eps, f.pairing,
+                       f.qn_out, f.kcache_w, f.vcache_w, 0u, n_heads, n_kv_heads, q_stride,
+                       kv_stride, rt);
+  else
+    hipLaunchKernelGGL((qk_prologue_kernel<64, true>), dim3(n_seqs), dim3(kPrologueThreads), 0,
+                       st, f.q_raw, f.k_raw, f.v_raw, f.gq, f.gk, f.inv_freq, f.eps, f.pairing,
+                       f.qn_out, f.kcache_w, f.vcache_w, 0u, n_heads, n_kv_heads, q_stride,
+                       kv_stride, rt);
   return hipGetLastError();
 }
 

@@ -48,6 +48,10 @@ export const hip = Deno.dlopen(Deno.env.get("FLOCK_ATTN_LIB") ?? "libflock_attn.
     parameters: [P, P, P, P, P, P, U32, U32, U32, U32, U32, P, U64],
     result: I32,
   },
+  flk_decode_layer_ragged: {
+    parameters: [P, P, P, P, P, P, F32, I32, P, P, P, P, P, P, U32, U32, U32, U32, U32, P, U64],
+    result: I32,
+  },
   // include/flock_q8.h
   flk_q8_matvec: { parameters: [P, P, P, P, U32, U32, U32], result: I32 },
   flk_q8_split: { parameters: ["buffer", U32, U32, "buffer", "buffer"], result: I32 },

@@ -251,6 +251,19 @@ def attn_decode_ragged(q, kcache, vcache, seq_row_off, n_keys, o, n_seqs: int, m
                                        n_kv_heads, head_dim, w, nb), "flk_attn_decode_ragged")
 
 
+def decode_layer_ragged(q_raw, k_raw, v_raw, gq, gk, inv_freq, eps: float, pairing, qn_out,
+                        kcache, vcache, seq_row_off, n_keys, o, n_seqs: int, max_n_keys: int,
+                        n_heads: int, n_kv_heads: int, head_dim: int, ws) -> None:
+    """One decode step for every sequence of a ragged batch (flk_decode_layer_ragged):
+    sequence b's new token is at position n_keys[b] - 1 of its cache rows."""
+    w, nb = _ws(ws)
+    check(lib().flk_decode_layer_ragged(ptr(q_raw), ptr(k_raw), ptr(v_raw), ptr(gq), ptr(gk),
+                                        ptr(inv_freq), eps, _pairing(pairing), ptr(qn_out),
+                                        ptr(kcache), ptr(vcache), ptr(seq_row_off), ptr(n_keys),
+                                        ptr(o), n_seqs, max_n_keys, n_heads, n_kv_heads,
+                                        head_dim, w, nb), "flk_decode_layer_ragged")
+
+
 # ------------------------------------------------------------ Q8_0 projections
 def q8_split(packed, n_rows: int, n_cols: int):
     """splitQ8 (kernels/lib.ts:141-156) on the host: GGUF Q8_0 bytes -> (qs int8, scales f16 bits)."""

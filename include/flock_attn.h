@@ -200,7 +200,8 @@ int32_t flk_decode_layer_noalloc(const float* q_raw, const float* k_raw, const f
  * are DEVICE arrays (8- and 4-byte aligned), so the library cannot check
  * their contents: rows seq_row_off[b] .. seq_row_off[b] + n_keys[b] - 1 must
  * lie inside kcache and vcache. max_n_keys bounds every n_keys[b] (larger
- * values are clamped to it). Up to 2048 sequences run on persistent workgroups that take
+ * values are clamped to it: such a sequence attends its first max_n_keys
+ * rows). Up to 2048 sequences run on persistent workgroups that take
  * the batch's (sequence, split) pieces from a counter kept in the workspace
  * (reset by the call itself); results are the same bits on every call. */
 int32_t flk_attn_decode_ragged(const float* q, const float* kcache, const float* vcache,
@@ -208,6 +209,34 @@ int32_t flk_attn_decode_ragged(const float* q, const float* kcache, const float*
                                uint32_t n_seqs, uint32_t max_n_keys, uint32_t n_heads,
                                uint32_t n_kv_heads, uint32_t head_dim, void* ws,
                                uint64_t ws_bytes);
+
+/* Extension, no reference counterpart: Layer.encode's attention slice
+ * (layer.ts:571-630) for n_seqs independent sequences in one call -- the
+ * per-token step of flk_decode_layer applied to every sequence of a batch
+ * (the reference runs one sequence per Layer, layer.ts:203-204).
+ * q_raw, qn_out, o: [n_seqs][n_heads][head_dim]; k_raw, v_raw:
+ * [n_seqs][n_kv_heads][head_dim]. n_keys[b] counts sequence b's keys AFTER
+ * this step: its new token sits at position pos_b = n_keys[b] - 1, q and k
+ * are normed (gains gq, gk) and rotated at pos_b, k (normed, rotated) and v
+ * (raw) are written to cache row seq_row_off[b] + pos_b, and the attention
+ * covers the rows seq_row_off[b] .. seq_row_off[b] + pos_b. n_keys[b] == 0
+ * marks an idle sequence: its qn and o rows are zeros and nothing is written
+ * to the caches. n_keys[b] > max_n_keys (the reference's "KV cache full",
+ * layer.ts:575, which the library cannot see on the host: the counts live
+ * in device memory) is refused on the device: that sequence's qn and o rows
+ * are NaN and nothing is written to the caches. Layouts, alignment,
+ * workspace (flk_call_workspace_bytes(FLK_CALL_RAGGED, ...)) and the
+ * conditions on seq_row_off are those of flk_attn_decode_ragged. Launches:
+ * the prologue (one workgroup per sequence; it also resets the batch's item
+ * counters), then flk_attn_decode_ragged's attention and merge. qn and the
+ * cache rows are bit-identical to flk_decode_layer's for each sequence. */
+int32_t flk_decode_layer_ragged(const float* q_raw, const float* k_raw, const float* v_raw,
+                                const float* gq, const float* gk, const float* inv_freq,
+                                float eps, int32_t pairing, float* qn_out, float* kcache,
+                                float* vcache, const uint64_t* seq_row_off,
+                                const uint32_t* n_keys, float* o, uint32_t n_seqs,
+                                uint32_t max_n_keys, uint32_t n_heads, uint32_t n_kv_heads,
+                                uint32_t head_dim, void* ws, uint64_t ws_bytes);
 
 #ifdef __cplusplus
 }

@@ -1,67 +1,11 @@
-"""Parity metrics and the bar the GPU path is held to.
-
-The bar (max-abs 2e-5 and max-rel 1e-4 against the CPU oracle, f32):
-  * max |gpu - oracle| <= 2e-5, always;
-  * relErr(gpu, oracle, floor 1e-3) <= 1e-4 -- the metric and floor of
-    test_ops.ts:343-353 -- or, where that per-element ratio is dominated by
-    outputs that cancel toward zero, the GPU must be about as close to the
-    exact (float64) result as the oracle itself: its largest absolute error
-    against the exact result at most 2x the oracle's own (+1e-7). With N(0,1)
-    inputs the oracle's serial f32 sums are already ~4e-4 (relErr) from the
-    exact result on such elements, so no f32 kernel that sums in a different
-    order can meet 1e-4 against it on every element; the 2x rule still fails a
-    dropped term, a wrong index or a lost rescale by orders of magnitude
-    (tests/test_parity_bar.py plants each of those in the oracle).
-Every call returns the measured numbers so tests can print them.
-"""
+"""Parity helpers for the tests: the bar itself lives in oracle/parity.py
+(shared with bench.py's CPU leg); printing and recording are here."""
 from __future__ import annotations
 
 import numpy as np
 
-import oracle
-
-MAX_ABS = 2e-5
-MAX_REL = 1e-4
-REL_FLOOR = 1e-3
-
-
-def metrics(gpu, orc, f64=None) -> dict:
-    gpu = np.asarray(gpu, np.float32)
-    orc = np.asarray(orc, np.float32)
-    m = {
-        "max_abs": float(np.max(np.abs(gpu.astype(np.float64) - orc))),
-        "rel": oracle.rel_err(gpu, orc, REL_FLOOR),
-        "abs_scaled": oracle.abs_err_scaled(gpu, orc, max(oracle.amax(orc), 1e-30)),
-    }
-    if f64 is not None:
-        f64 = np.asarray(f64, np.float64)
-        ref = f64.astype(np.float32)
-        m["gpu_vs_f64"] = oracle.rel_err(gpu, ref, REL_FLOOR)
-        m["oracle_vs_f64"] = oracle.rel_err(orc, ref, REL_FLOOR)
-        m["gpu_abs_vs_f64"] = float(np.max(np.abs(gpu - f64)))
-        m["oracle_abs_vs_f64"] = float(np.max(np.abs(orc - f64)))
-    return m
-
-
-def meets_bar(m: dict) -> bool:
-    if m["max_abs"] > MAX_ABS:
-        return False
-    if m["rel"] <= MAX_REL:
-        return True
-    if "oracle_vs_f64" not in m:
-        return False
-    return m["gpu_abs_vs_f64"] <= 2 * m["oracle_abs_vs_f64"] + 1e-7
-
-
-def clause(m: dict) -> str:
-    """Which part of the bar decided: 'literal' (max-abs 2e-5 and relErr
-    1e-4 both hold), '2x-oracle' (relErr above 1e-4, passed on the distance
-    from float64), or 'fail'."""
-    if m["max_abs"] > MAX_ABS:
-        return "fail"
-    if m["rel"] <= MAX_REL:
-        return "literal"
-    return "2x-oracle" if meets_bar(m) else "fail"
+from oracle.parity import (MAX_ABS, MAX_REL, REL_FLOOR, argmax_rows, clause, meets_bar,  # noqa: F401
+                           metrics, projection_ids)
 
 
 def fmt(m: dict) -> str:
@@ -82,25 +26,6 @@ def record(case: str, m: dict, **extra) -> None:
             f.write(json.dumps(row) + "\n")
 
 
-def argmax_rows(x: np.ndarray, rows: int) -> np.ndarray:
-    """Per-row argmax, lowest index winning ties (head_ref.ts:65-74)."""
-    x = np.asarray(x, np.float32).reshape(rows, -1)
-    return np.array([oracle.argmax(r) for r in x])
-
-
 def top2_margin(x: np.ndarray, rows: int) -> float:
     x = np.sort(np.asarray(x, np.float32).reshape(rows, -1), axis=1)
     return float(np.min(x[:, -1] - x[:, -2]))
-
-
-def projection_ids(o_flat: np.ndarray, vocab: int = 4096, seed: int = 7) -> tuple[int, float]:
-    """Downstream token id: argmax of a seeded f32 projection W [vocab, len(o)] . o.
-
-    The same CPU code evaluates it for the GPU and the oracle outputs; returns
-    (id, top-2 margin).
-    """
-    o = np.asarray(o_flat, np.float32).ravel()
-    w = np.random.default_rng(seed).standard_normal((vocab, o.size), dtype=np.float32)
-    logits = (w @ o).astype(np.float32)
-    s = np.sort(logits)
-    return oracle.argmax(logits), float(s[-1] - s[-2])

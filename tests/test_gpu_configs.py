@@ -1,8 +1,9 @@
 """The benchmark configurations at their full sizes, on the GPU, against the oracle.
 
 Decode over 513 keys (the new token's row appended at 512); decode at 32769
-keys with the fused prologue (one layer of 28); the 64-sequence ragged batch,
-every sequence against the oracle; causal prefill of 2048 tokens; a 64-token
+keys with the fused prologue (one layer of 28); the 64-sequence ragged decode
+step (prologue, append and attention for every sequence in one call), every
+sequence against the oracle; causal prefill of 2048 tokens; a 64-token
 chunk onto a 32768-key cache (one layer of 28). Inputs are N(0, 1) (gains N(1, 0.1)) like
 the benchmark's; each output is held to the parity bar against the oracle and
 the float64 closed form, and each case's numbers are recorded (parity.record:
@@ -157,37 +158,51 @@ def test_chunk_onto_32k_cache(rng):
 
 
 def test_ragged_batch_of_64(rng):
-    # 64 sequences, n_keys ~ U[1025, 16385], one call; every
-    # sequence against the oracle's attnRef (ops_ref.ts:135-174) and the
-    # float64 closed form.
+    # 64 sequences, n_keys ~ U[1025, 16385] after the step, one call of the
+    # whole decode step (flk_decode_layer_ragged): per sequence norm + RoPE
+    # (theta 1e6) of the new q and k at position n_keys - 1, the append, and
+    # attention. Every sequence against the oracle's layer_attn_decode
+    # (layer_ref.ts:46-70, attnRef ops_ref.ts:135-174) and the float64 closed
+    # form; qn and the appended cache rows bit-identical.
     B = 64
     lens = (rng.integers(1024, 16385, B) + 1).astype(np.uint32)
     offs = np.concatenate([[0], np.cumsum(lens.astype(np.uint64))[:-1]]).astype(np.uint64)
     rows = int(lens.astype(np.uint64).sum())
-    kc, vc = randn(rng, rows * HKV * D), randn(rng, rows * HKV * D)
-    q = randn(rng, B * H * D)
+    row = HKV * D
+    kc, vc = randn(rng, rows * row), randn(rng, rows * row)
+    q, k, v = randn(rng, B * H * D), randn(rng, B * row), randn(rng, B * row)
+    gq, gk = gains(rng)
+    inv = ops.rope_inv_freq(D, 1e6)
     kcb, vcb = dev(kc), dev(vc)
     ws = ops.Workspace(H, HKV, D, int(lens.max()), 0, B)
-    o = ops.DeviceBuffer(B * H * D * 4)
-    ops.attn_decode_ragged(dev(q), kcb, vcb, ops.DeviceBuffer.from_array(offs),
-                           ops.DeviceBuffer.from_array(lens), o, B, int(lens.max()), H, HKV, D, ws)
+    qn, o = ops.DeviceBuffer(B * H * D * 4), ops.DeviceBuffer(B * H * D * 4)
+    ops.decode_layer_ragged(dev(q), dev(k), dev(v), dev(gq), dev(gk), dev(inv), EPS, "neox", qn,
+                            kcb, vcb, ops.DeviceBuffer.from_array(offs),
+                            ops.DeviceBuffer.from_array(lens), o, B, int(lens.max()), H, HKV, D,
+                            ws)
     ops.sync()
     got = o.download(B * H * D).reshape(B, H * D)
+    got_qn = qn.download(B * H * D).reshape(B, H * D)
     oracle.set_threads(min(16, os.cpu_count() or 1))
-    row = HKV * D
     worst, ties, ids_equal = None, 0, 0
     for b in range(B):
         s, n = int(offs[b]) * row, int(lens[b])
-        qb = q[b * H * D:(b + 1) * H * D]
-        kb, vb = kc[s:s + n * row], vc[s:s + n * row]
-        want = oracle.attn(qb, kb, vb, H, HKV, D, n)
-        m = metrics(got[b], want, cf.attention(qb, kb, vb, H, HKV, D, 1, n - 1))
+        kb, vb = kc[s:s + n * row], vc[s:s + n * row]  # views: the oracle appends in place
+        want_qn, want = oracle.layer_attn_decode(q[b * H * D:(b + 1) * H * D],
+                                                 k[b * row:(b + 1) * row],
+                                                 v[b * row:(b + 1) * row], gq, gk, inv, kb, vb,
+                                                 n - 1, H, HKV, D)
+        assert np.array_equal(got_qn[b], want_qn), b
+        last = (int(offs[b]) + n - 1) * row
+        assert np.array_equal(kcb.download(row, offset_bytes=last * 4), kc[last:last + row]), b
+        assert np.array_equal(vcb.download(row, offset_bytes=last * 4), vc[last:last + row]), b
+        m = metrics(got[b], want, cf.attention(want_qn, kb, vb, H, HKV, D, 1, n - 1))
         assert meets_bar(m), (b, n, fmt(m))
         ids = check_ids(f"ragged sequence {b}", got[b], want, H, m["max_abs"])
         ties += ids["near_tie_rows"]
         ids_equal += int(ids["projection_id_equal"])
         if worst is None or m["rel"] > worst[1]["rel"]:
             worst = (b, m)
-    record("ragged decode, 64 sequences (worst of 64)", worst[1], seq=worst[0],
+    record("ragged decode step, 64 sequences (worst of 64)", worst[1], seq=worst[0],
            n_keys=int(lens[worst[0]]), sum_n_keys=rows, rows=B * H, near_tie_rows=ties,
            projection_ids_equal=ids_equal, sequences=B)

@@ -552,6 +552,163 @@ def test_decode_ragged_repeats_bit_for_bit(rng):
     assert all(np.array_equal(x, outs[0]) for x in outs[1:])
 
 
+# Past the bound: flk_attn_decode_ragged clamps n_keys[b] > max_n_keys, so such
+# a sequence attends its first max_n_keys rows. Both sides of the persistent
+# kernel's 2048-sequence limit.
+@pytest.mark.parametrize("n_seqs", [40, 2100])
+def test_decode_ragged_clamps_counts_past_the_bound(rng, n_seqs):
+    H, Hkv, d = 16, 8, 128
+    maxn = 300
+    lens = rng.integers(1, maxn + 1, n_seqs).astype(np.uint32)
+    over = [1, n_seqs // 2, n_seqs - 1]
+    lens[over] = [maxn + 1, maxn + 57, 4 * maxn]
+    offs = (np.arange(n_seqs, dtype=np.uint64) * np.uint64(4 * maxn + 2))
+    rows = int(offs[-1]) + 4 * maxn + 2
+    kc, vc = randn(rng, rows * Hkv * d), randn(rng, rows * Hkv * d)
+    q = randn(rng, n_seqs * H * d)
+    ws = ops.Workspace(H, Hkv, d, maxn, 0, n_seqs)
+    o = empty(n_seqs * H * d)
+    ops.attn_decode_ragged(dev(q), dev(kc), dev(vc), ops.DeviceBuffer.from_array(offs),
+                           ops.DeviceBuffer.from_array(lens), o, n_seqs, maxn, H, Hkv, d, ws)
+    got = get(o, n_seqs * H * d).reshape(n_seqs, H * d)
+    row = Hkv * d
+    for b in over + [0, 2]:
+        n = min(int(lens[b]), maxn)
+        s = int(offs[b]) * row
+        qb = q[b * H * d:(b + 1) * H * d]
+        want = oracle.attn(qb, kc[s:s + n * row], vc[s:s + n * row], H, Hkv, d, n)
+        m = metrics(got[b], want, cf.attention(qb, kc[s:s + n * row], vc[s:s + n * row], H, Hkv,
+                                               d, 1, n - 1))
+        assert meets_bar(m), (b, int(lens[b]), fmt(m))
+
+
+# ------------------------------------------------------- ragged layer step --
+def _ragged_layer_vs_oracle(rng, H, Hkv, d, lens, pairing="neox", max_n_keys=None):
+    """flk_decode_layer_ragged against oracle.layer_attn_decode per sequence
+    (layer_ref.ts:46-70 at position n_keys[b] - 1 of that sequence's rows):
+    qn and every cache row bit-identical, o to the parity bar; idle
+    sequences (0 keys) give zero rows and refused ones (past max_n_keys) NaN
+    rows, and neither writes to the caches."""
+    lens = np.asarray(lens, np.uint32)
+    B = len(lens)
+    maxn = int(lens.max()) if max_n_keys is None else int(max_n_keys)
+    span = np.minimum(lens.astype(np.int64), maxn) + 3  # rows per sequence, gaps between
+    offs = np.concatenate([[0], np.cumsum(span)[:-1]]).astype(np.uint64)
+    rows = int(offs[-1]) + int(span[-1])
+    row = Hkv * d
+    kc0, vc0 = randn(rng, rows * row), randn(rng, rows * row)
+    q, k, v = randn(rng, B * H * d), randn(rng, B * row), randn(rng, B * row)
+    gq, gk = rng.normal(1, 0.1, d).astype(np.float32), rng.normal(1, 0.1, d).astype(np.float32)
+    inv = oracle.rope_inv_freq(d, 1e6)
+    kc, vc = dev(kc0), dev(vc0)
+    qn, o = empty(B * H * d), empty(B * H * d)
+    ws = ops.Workspace(H, Hkv, d, maxn, 0, B)
+    ops.decode_layer_ragged(dev(q), dev(k), dev(v), dev(gq), dev(gk), dev(inv), EPS, pairing, qn,
+                            kc, vc, ops.DeviceBuffer.from_array(offs),
+                            ops.DeviceBuffer.from_array(lens), o, B, maxn, H, Hkv, d, ws)
+    got_o = get(o, B * H * d).reshape(B, H * d)
+    got_qn = qn.download(B * H * d).reshape(B, H * d)
+    got_kc, got_vc = kc.download(rows * row), vc.download(rows * row)
+    kco, vco = kc0.copy(), vc0.copy()
+    for b in range(B):
+        n = int(lens[b])
+        if n == 0:
+            assert np.all(got_o[b] == 0) and np.all(got_qn[b] == 0), b
+            continue
+        if n > maxn:
+            assert np.all(np.isnan(got_o[b])) and np.all(np.isnan(got_qn[b])), b
+            continue
+        s = int(offs[b]) * row
+        kb, vb = kco[s:s + n * row], vco[s:s + n * row]  # views: the oracle appends in place
+        hq, hk = slice(b * H * d, (b + 1) * H * d), slice(b * row, (b + 1) * row)
+        want_qn, want_o = oracle.layer_attn_decode(q[hq], k[hk], v[hk], gq, gk, inv, kb, vb,
+                                                   n - 1, H, Hkv, d, EPS, pairing)
+        assert np.array_equal(got_qn[b], want_qn), b
+        m = metrics(got_o[b], want_o, cf.attention(want_qn, kb, vb, H, Hkv, d, 1, n - 1))
+        assert meets_bar(m), (b, n, fmt(m))
+    assert np.array_equal(got_kc, kco)
+    assert np.array_equal(got_vc, vco)
+
+
+@pytest.mark.parametrize("H,Hkv,d", [(16, 8, 128), (16, 8, 64), (12, 4, 64), (10, 2, 128),
+                                     (8, 1, 128), (32, 8, 128)])
+def test_decode_layer_ragged_head_layouts(rng, H, Hkv, d):
+    G = H // Hkv
+    kh = next(k for k in (8, 4, 2, 1) if Hkv % k == 0)
+    kpi = (512 // (d // 4)) // kh * (4 if G <= 4 else 2)
+    _ragged_layer_vs_oracle(rng, H, Hkv, d, [1, kpi - 1, kpi, kpi + 1, 2 * kpi + 3, 0, 1500, 2])
+
+
+@pytest.mark.parametrize("pairing", ["neox", "norm"])
+def test_decode_layer_ragged_positions_past_32k(rng, pairing):
+    # RoPE at large positions (the reference's theta 1e6 at 32768+), one
+    # sequence on each side of a block edge.
+    _ragged_layer_vs_oracle(rng, 16, 8, 128, [32769, 33000, 5], pairing)
+
+
+def test_decode_layer_ragged_single_sequence(rng):
+    # One sequence takes the single-sequence split plan; same results as a batch.
+    _ragged_layer_vs_oracle(rng, 16, 8, 128, [4097])
+
+
+def test_decode_layer_ragged_refuses_counts_past_the_bound(rng):
+    # The counts live in device memory, so the host cannot throw "KV cache
+    # full" (layer.ts:575): a sequence past max_n_keys gets NaN rows and no
+    # append; its neighbours are unaffected.
+    _ragged_layer_vs_oracle(rng, 16, 8, 128, [700, 1001, 0, 1000, 5000, 3], max_n_keys=1000)
+
+
+@pytest.mark.parametrize("n_seqs", [2048, 2100])
+def test_decode_layer_ragged_many_sequences(rng, n_seqs):
+    # Both sides of the persistent kernel's limit, with idle, one-key and
+    # refused sequences among them.
+    lens = rng.integers(0, 41, n_seqs).astype(np.uint32)
+    lens[:4] = [0, 1, 40, 41]
+    _ragged_layer_vs_oracle(rng, 16, 8, 128, lens, max_n_keys=40)
+
+
+def test_decode_layer_ragged_graph_replay(rng):
+    # The prologue launch also resets the batch kernel's item counters; a
+    # captured step replays that reset, so every replay gives the eager bits
+    # (each replay rewrites the same cache rows with the same values).
+    H, Hkv, d = 16, 8, 128
+    lens = np.array([2500, 0, 900, 4097, 1], np.uint32)
+    B = len(lens)
+    offs = np.concatenate([[0], np.cumsum(lens)[:-1]]).astype(np.uint64)
+    rows = int(lens.sum())
+    kc, vc = dev(randn(rng, rows * Hkv * d)), dev(randn(rng, rows * Hkv * d))
+    q, k, v = dev(randn(rng, B * H * d)), dev(randn(rng, B * Hkv * d)), dev(randn(rng, B * Hkv * d))
+    gq, gk = dev(rng.normal(1, 0.1, d)), dev(rng.normal(1, 0.1, d))
+    inv = dev(oracle.rope_inv_freq(d, 1e6))
+    offs_d, lens_d = ops.DeviceBuffer.from_array(offs), ops.DeviceBuffer.from_array(lens)
+    maxn = int(lens.max())
+    ws = ops.Workspace(H, Hkv, d, maxn, 0, B)
+    qn, o = empty(B * H * d), empty(B * H * d)
+    call = lambda: ops.decode_layer_ragged(q, k, v, gq, gk, inv, EPS, "neox", qn, kc, vc, offs_d,
+                                           lens_d, o, B, maxn, H, Hkv, d, ws)
+    st = ops.Stream()
+    ops.set_stream(st)
+    try:
+        call()
+        ops.sync()
+        eager = get(o, B * H * d)
+        eager_kc = kc.download(rows * Hkv * d)
+        with ops.Graph() as g:
+            call()
+        for i in range(3):
+            o.zero()  # eager, between replays
+            g.launch()
+            ops.sync()
+            assert np.array_equal(get(o, B * H * d), eager), i
+            assert np.array_equal(kc.download(rows * Hkv * d), eager_kc), i
+            call()  # an eager call between replays
+            ops.sync()
+        g.free()
+    finally:
+        ops.set_stream(None)
+        st.free()
+
+
 # ------------------------------------------------------------ golden fixtures --
 def test_golden_fixtures_on_gpu():
     # tests/golden/golden.npz: seeded inputs with the oracle's outputs and the
