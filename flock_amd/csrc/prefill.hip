@@ -41,109 +41,14 @@
 //   split:  too few q tiles to fill the GPU (chunked prefill onto a long
 //           cache): work item (q tile, split) runs a range of key tiles and
 //           writes an (m, l, acc) partial that prefill_merge_kernel combines.
-#include "common.hpp"
+#include "prefill.hpp"
 
 namespace flk {
 
-typedef float floatx4 __attribute__((ext_vector_type(4)));
-
-constexpr int kRows = 64;    // query-head rows per q tile
-constexpr int kBK = 64;      // keys per tile
-constexpr int kPThreads = 512;  // 8 waves: 4 row blocks x 2 key halves
-constexpr int kHalfKB = 2;      // 16-key blocks per wave per tile
-constexpr uint32_t kMinPairedWG = 192;    // paired mode when it yields this many
-constexpr uint32_t kTargetSplitWG = 256;  // split mode aims at one workgroup per CU
-constexpr uint32_t kMinKtPerSplit = 2;
-#ifndef FLK_PREFILL_OPAD
-#define FLK_PREFILL_OPAD 4  // padding of the combine's o rows in LDS (floats)
+#ifndef FLK_PREFILL_KPERM
+#define FLK_PREFILL_KPERM 1  // K rows stored with chunks 8..15 and 16..23 swapped (D = 128)
 #endif
-#ifndef FLK_PREFILL_AHEAD
-#define FLK_PREFILL_AHEAD 1  // operand groups read from LDS ahead of their MFMAs
-#endif
-
-struct PrefillArgs {
-  const float* q;
-  const float* kcache;
-  const float* vcache;
-  float* o;
-  float2* part_ml;   // [slot][kRows]
-  float* part_acc;   // [slot][kRows][D]
-  uint32_t n_heads, n_kv_heads, group;
-  uint32_t n_queries, pos0;
-  uint32_t q_per_tile, n_qtiles;
-  uint32_t paired, work_per_kvh;
-  uint32_t kt_per_split, max_splits;
-  float scale_log2e;  // fr(1/sqrt(d) * log2(e)): scores in base-2 units
-};
-
-__host__ __device__ __forceinline__ uint32_t qtile_kt(uint32_t qt, uint32_t q_per_tile,
-                                                      uint32_t n_queries, uint32_t pos0) {
-  const uint32_t q_end = (qt + 1) * q_per_tile < n_queries ? (qt + 1) * q_per_tile : n_queries;
-  return (pos0 + q_end + kBK - 1) / kBK;
-}
-
-// gfx9 buffer-descriptor word 3 for untyped 32-bit-element loads.
-constexpr int kBufferWord3 = 0x00020000;
-
-// Rows of key tile kt of `cache` (K or V) into registers: NPF float4 per
-// thread. The descriptor covers the tile's live rows only (rows from kt * kBK,
-// at most kBK, at most up to the last key), so a row past the last key reads
-// as 0.
-template <int D, int NPF = kBK * D / 4 / kPThreads>
-__device__ __forceinline__ void load_rows(float4 (&pr)[NPF], const float* cache,
-                                          const PrefillArgs& a, uint32_t kvh, uint32_t kt,
-                                          uint32_t n_keys_total, int tid) {
-  const uint32_t key0 = kt * kBK;
-  const uint32_t rows = min(n_keys_total - key0, (uint32_t)kBK);
-  const uint32_t row_bytes = a.n_kv_heads * D * 4;
-  const size_t base = (size_t)key0 * row_bytes + (size_t)kvh * D * 4;
-  const uint32_t n_bytes = (rows - 1) * row_bytes + D * 4;
-  const __amdgpu_buffer_rsrc_t rr = __builtin_amdgcn_make_buffer_rsrc(
-      const_cast<char*>(reinterpret_cast<const char*>(cache) + base), 0, n_bytes, kBufferWord3);
-  typedef float f4v __attribute__((ext_vector_type(4)));
-#pragma unroll
-  for (int i = 0; i < NPF; i++) {
-    const int f = tid + kPThreads * i;
-    const int r = f / (D / 4), c4 = f % (D / 4);
-    const f4v x = __builtin_bit_cast(
-        f4v, __builtin_amdgcn_raw_buffer_load_b128(rr, r * (int)row_bytes + 16 * c4, 0, 0));
-    pr[i] = make_float4(x.x, x.y, x.z, x.w);
-  }
-}
-
-// K and V rows of key tile kt into registers.
-template <int D, int NPF = kBK * D / 4 / kPThreads>
-__device__ __forceinline__ void load_tile(float4 (&pk)[NPF], float4 (&pv)[NPF],
-                                          const PrefillArgs& a, uint32_t kvh, uint32_t kt,
-                                          uint32_t n_keys_total, int tid) {
-  load_rows<D>(pk, a.kcache, a, kvh, kt, n_keys_total, tid);
-  load_rows<D>(pv, a.vcache, a, kvh, kt, n_keys_total, tid);
-}
-
-template <int D, int NPF = kBK * D / 4 / kPThreads>
-__device__ __forceinline__ void store_k(const float4 (&pk)[NPF], float* k_lds, int tid) {
-#pragma unroll
-  for (int i = 0; i < NPF; i++) {
-    const int f = tid + kPThreads * i;
-    *reinterpret_cast<float4*>(&k_lds[(f / (D / 4)) * (D + 4) + 4 * (f % (D / 4))]) = pk[i];
-  }
-}
-template <int D, int NPF = kBK * D / 4 / kPThreads>
-__device__ __forceinline__ void store_v(const float4 (&pv)[NPF], float* v_lds, int tid) {
-#pragma unroll
-  for (int i = 0; i < NPF; i++) {
-    const int f = tid + kPThreads * i;
-    *reinterpret_cast<float4*>(&v_lds[(f / (D / 4)) * D + 4 * (f % (D / 4))]) = pv[i];
-  }
-}
-
-// Registers of one key tile into one LDS buffer (K rows padded to D + 4).
-template <int D, int NPF = kBK * D / 4 / kPThreads>
-__device__ __forceinline__ void store_tile(const float4 (&pk)[NPF], const float4 (&pv)[NPF],
-                                           float* k_lds, float* v_lds, int tid) {
-  store_k<D>(pk, k_lds, tid);
-  store_v<D>(pv, v_lds, tid);
-}
+constexpr bool kKPerm = FLK_PREFILL_KPERM != 0;
 
 // This lane's row of q tile qt in the B-operand layout of S^T = K Q^T (D/4
 // floats from dim (D/4) * lg), pre-multiplied by scale * log2(e) so that S^T
@@ -233,7 +138,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   // tile kt + 1 is stored into the other one and tile kt + 2 loads into
   // registers; one barrier per tile separates the two.
   __syncthreads();  // LDS may still hold the previous q tile's merge data
-  store_tile<D>(pk, pv, k_lds, v_lds, tid);
+  store_tile<D, kKPerm>(pk, pv, k_lds, v_lds, tid);
   load_tile<D>(pk, pv, a, kvh, kt0 + 1 < kt1 ? kt0 + 1 : kt0, n_keys_total, tid);
   __syncthreads();
 
@@ -243,7 +148,9 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   constexpr int kAhead = FLK_PREFILL_AHEAD;
   constexpr int NG = DS / 4;        // S: groups of 4 k-steps (one float4 per chain)
   constexpr int NST = kHalfKB * 4;  // PV: k-steps of 4 keys
-  const float* kr0 = &k_lds[((half * kHalfKB) * 16 + lc) * LDK + DS * lg];
+  // Lane group lg reads chunks 8 lg .. 8 lg + 7 (D = 128) of its key rows.
+  const float* kr0 =
+      &k_lds[((half * kHalfKB) * 16 + lc) * LDK + 4 * k_chunk_pos<D, kKPerm>((DS / 4) * lg)];
   const float* vr0 = &v_lds[((half * kHalfKB) * 16 + 4 * lg) * D + CB * lc];
   auto k_group = [&](const float* kt_lds_base, int g, int b) {
     return *reinterpret_cast<const floatx4*>(kt_lds_base + b * 16 * LDK + 4 * g);
@@ -286,7 +193,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
       // requested right after each half (the last one is simply loaded again
       // at the end).
       if (g == NG / 4 && kt + 1 < kt1) {
-        store_k<D>(pk, k_lds + (buf ^ 1) * (kBK * LDK), tid);
+        store_k<D, kKPerm>(pk, k_lds + (buf ^ 1) * (kBK * LDK), tid);
         load_rows<D>(pk, a.kcache, a, kvh, kt + 2 < kt1 ? kt + 2 : kt + 1, n_keys_total, tid);
       }
       if (g == 3 * NG / 4 && kt + 1 < kt1) {
@@ -530,7 +437,8 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
 // ------------------------------------------------------------------ plan ----
 PrefillPlan prefill_plan(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                          uint32_t n_queries, uint32_t pos0) {
-  (void)head_dim;
+  if (prefill32_fits(n_heads, n_kv_heads, head_dim, n_queries))
+    return prefill32_plan(n_heads, n_kv_heads, n_queries, pos0);
   PrefillPlan p{};
   const uint32_t group = n_heads / n_kv_heads;
   p.rows_per_tile = kRows;
@@ -562,8 +470,9 @@ PrefillPlan prefill_plan(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_di
 
 uint64_t prefill_ws_bytes(const PrefillPlan& p, uint32_t head_dim) {
   if (p.partial_slots == 0) return 0;
-  return ws_align(p.partial_slots * kRows * sizeof(float2)) +
-         p.partial_slots * kRows * head_dim * sizeof(float);
+  const uint64_t rows = p.x32 ? p.rows_per_tile : kRows;
+  return ws_align(p.partial_slots * rows * sizeof(float2)) +
+         p.partial_slots * rows * head_dim * sizeof(float);
 }
 
 // Upper bound over every plan with n_queries <= max_queries and pos0 +
@@ -573,8 +482,8 @@ uint64_t prefill_ws_bytes(const PrefillPlan& p, uint32_t head_dim) {
 // * max_kt / kTargetSplitWG and ms = ceil(max_kt / ch) <= ceil(kTargetSplitWG /
 // n_kv_heads); also ms <= ceil(max_kt / kMinKtPerSplit) with max_kt <=
 // ceil(max_keys / kBK).
-uint64_t prefill_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                          uint32_t max_queries, uint32_t max_keys) {
+static uint64_t prefill16_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                                  uint32_t max_queries, uint32_t max_keys) {
   const uint32_t qpt = kRows / (n_heads / n_kv_heads);
   const uint64_t max_qt = (max_queries + qpt - 1) / qpt;
   uint64_t nqt = 0;  // most q tiles a split plan can have
@@ -588,6 +497,27 @@ uint64_t prefill_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_d
   PrefillPlan p{};
   p.partial_slots = nqt * ms * n_kv_heads;
   return prefill_ws_bytes(p, head_dim);
+}
+
+// Both kernels: calls with few query rows take the 64-row kernel, longer ones
+// (head_dim 128) the 128-row kernel.
+uint64_t prefill_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                          uint32_t max_queries, uint32_t max_keys) {
+  // The 64-row kernel serves only the calls the 128-row one does not take.
+  // (prefill32_fits: head_dim 128 and more than kRows query rows.)
+  uint32_t max_q16 = max_queries;
+  if (head_dim == 128 && max_q16 > kRows / (n_heads / n_kv_heads))
+    max_q16 = kRows / (n_heads / n_kv_heads);
+  uint64_t b = max_q16 ? prefill16_ws_bound(n_heads, n_kv_heads, head_dim, max_q16, max_keys) : 0;
+  if (prefill32_fits(n_heads, n_kv_heads, head_dim, max_queries)) {
+    PrefillPlan p{};
+    p.x32 = 1;
+    p.rows_per_tile = 128;
+    p.partial_slots = prefill32_slots_bound(n_heads, n_kv_heads, max_queries, max_keys);
+    const uint64_t b32 = prefill_ws_bytes(p, head_dim);
+    if (b32 > b) b = b32;
+  }
+  return b;
 }
 
 template <int D>
@@ -612,9 +542,10 @@ hipError_t launch_prefill(const float* q, const float* kcache, const float* vcac
   a.vcache = vcache;
   a.o = o;
   if (p.partial_slots > 0) {
+    const uint64_t rows = p.x32 ? p.rows_per_tile : kRows;
     char* w = static_cast<char*>(ws);
     a.part_ml = reinterpret_cast<float2*>(w);
-    a.part_acc = reinterpret_cast<float*>(w + ws_align(p.partial_slots * kRows * sizeof(float2)));
+    a.part_acc = reinterpret_cast<float*>(w + ws_align(p.partial_slots * rows * sizeof(float2)));
   }
   a.n_heads = n_heads;
   a.n_kv_heads = n_kv_heads;
@@ -627,7 +558,9 @@ hipError_t launch_prefill(const float* q, const float* kcache, const float* vcac
   a.work_per_kvh = p.work_per_kvh;
   a.kt_per_split = p.ktiles_per_split;
   a.max_splits = p.max_splits;
+  a.pieces = p.pieces;
   a.scale_log2e = (float)(1.4426950408889634 / sqrt((double)head_dim));
+  if (p.x32) return launch_prefill32(a, p, st);
   if (head_dim == 128) return launch_prefill_d<128>(a, p, st);
   return launch_prefill_d<64>(a, p, st);
 }

@@ -423,6 +423,38 @@ def test_prefill_causality_bit_identical(rng):
     assert np.sum(base[5:] != pert[5:]) > H * d
 
 
+# The same two properties on the 128-row kernel (head_dim 128, more than 64
+# query rows), unsplit and with a q tile cut into pieces over a long cache.
+@pytest.mark.parametrize("nq,pos0,at", [(200, 0, 150), (64, 5000, 30), (300, 40, 7)])
+def test_prefill32_causality_bit_identical(rng, nq, pos0, at):
+    H, Hkv, d = 16, 8, 128
+    nk = pos0 + nq
+    q = rand_unit(rng, nq * H * d)
+    k, v = rand_unit(rng, nk * Hkv * d), rand_unit(rng, nk * Hkv * d)
+    base = _prefill(q, k, v, H, Hkv, d, nq, pos0).reshape(nq, -1)
+    k2, v2 = k.copy(), v.copy()
+    idx = np.arange(Hkv * d)
+    key = pos0 + at
+    k2[key * Hkv * d + idx] = 9 + idx * 0.01
+    v2[key * Hkv * d + idx] = -7 - idx * 0.01
+    pert = _prefill(q, k2, v2, H, Hkv, d, nq, pos0).reshape(nq, -1)
+    assert np.array_equal(base[:at], pert[:at])
+    assert np.sum(base[at:] != pert[at:]) > H * d
+
+
+def test_prefill32_queries_match_decode(rng):
+    # test_head.ts:321-351 on the 128-row kernel: query `at` equals the decode
+    # reference over keys 0 .. at.
+    H, Hkv, d, nq = 16, 8, 128, 193
+    q = rand_unit(rng, nq * H * d)
+    k, v = rand_unit(rng, nq * Hkv * d), rand_unit(rng, nq * Hkv * d)
+    pre = _prefill(q, k, v, H, Hkv, d, nq, 0).reshape(nq, H * d)
+    for at in (0, 63, 64, 127, 128, 191, 192):
+        want = oracle.attn(q.reshape(nq, -1)[at], k[:(at + 1) * Hkv * d], v[:(at + 1) * Hkv * d],
+                           H, Hkv, d, at + 1)
+        assert oracle.abs_err_scaled(pre[at], want, oracle.amax(want)) < 2e-5
+
+
 def test_prefill_deterministic_across_runs(rng):
     H, Hkv, d, nq, pos0 = 16, 8, 128, 64, 5000
     nk = pos0 + nq
