@@ -281,8 +281,6 @@ struct PrefillPlan {
   uint32_t ktiles_per_split;
   uint32_t max_splits;      // splits of the heaviest q tile (split mode)
   uint64_t partial_slots;   // n_qtiles * max_splits * n_kv_heads when splitting
-  uint32_t x32;             // 1: the 128-row v_mfma_f32_32x32x2f32 kernel (prefill32.hip)
-  uint32_t pieces;          // x32: pieces per q-tile pair (1: no partials)
 };
 PrefillPlan prefill_plan(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                          uint32_t n_queries, uint32_t pos0);

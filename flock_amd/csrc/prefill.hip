@@ -437,8 +437,6 @@ __global__ __launch_bounds__(256) void prefill_merge_kernel(PrefillArgs a) {
 // ------------------------------------------------------------------ plan ----
 PrefillPlan prefill_plan(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
                          uint32_t n_queries, uint32_t pos0) {
-  if (prefill32_fits(n_heads, n_kv_heads, head_dim, n_queries))
-    return prefill32_plan(n_heads, n_kv_heads, n_queries, pos0);
   PrefillPlan p{};
   const uint32_t group = n_heads / n_kv_heads;
   p.rows_per_tile = kRows;
@@ -470,9 +468,8 @@ PrefillPlan prefill_plan(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_di
 
 uint64_t prefill_ws_bytes(const PrefillPlan& p, uint32_t head_dim) {
   if (p.partial_slots == 0) return 0;
-  const uint64_t rows = p.x32 ? p.rows_per_tile : kRows;
-  return ws_align(p.partial_slots * rows * sizeof(float2)) +
-         p.partial_slots * rows * head_dim * sizeof(float);
+  return ws_align(p.partial_slots * kRows * sizeof(float2)) +
+         p.partial_slots * kRows * head_dim * sizeof(float);
 }
 
 // Upper bound over every plan with n_queries <= max_queries and pos0 +
@@ -482,8 +479,8 @@ uint64_t prefill_ws_bytes(const PrefillPlan& p, uint32_t head_dim) {
 // * max_kt / kTargetSplitWG and ms = ceil(max_kt / ch) <= ceil(kTargetSplitWG /
 // n_kv_heads); also ms <= ceil(max_kt / kMinKtPerSplit) with max_kt <=
 // ceil(max_keys / kBK).
-static uint64_t prefill16_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                                  uint32_t max_queries, uint32_t max_keys) {
+uint64_t prefill_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
+                          uint32_t max_queries, uint32_t max_keys) {
   const uint32_t qpt = kRows / (n_heads / n_kv_heads);
   const uint64_t max_qt = (max_queries + qpt - 1) / qpt;
   uint64_t nqt = 0;  // most q tiles a split plan can have
@@ -497,27 +494,6 @@ static uint64_t prefill16_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32
   PrefillPlan p{};
   p.partial_slots = nqt * ms * n_kv_heads;
   return prefill_ws_bytes(p, head_dim);
-}
-
-// Both kernels: calls with few query rows take the 64-row kernel, longer ones
-// (head_dim 128) the 128-row kernel.
-uint64_t prefill_ws_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                          uint32_t max_queries, uint32_t max_keys) {
-  // The 64-row kernel serves only the calls the 128-row one does not take.
-  // (prefill32_fits: head_dim 128 and more than kRows query rows.)
-  uint32_t max_q16 = max_queries;
-  if (head_dim == 128 && max_q16 > kRows / (n_heads / n_kv_heads))
-    max_q16 = kRows / (n_heads / n_kv_heads);
-  uint64_t b = max_q16 ? prefill16_ws_bound(n_heads, n_kv_heads, head_dim, max_q16, max_keys) : 0;
-  if (prefill32_fits(n_heads, n_kv_heads, head_dim, max_queries)) {
-    PrefillPlan p{};
-    p.x32 = 1;
-    p.rows_per_tile = 128;
-    p.partial_slots = prefill32_slots_bound(n_heads, n_kv_heads, max_queries, max_keys);
-    const uint64_t b32 = prefill_ws_bytes(p, head_dim);
-    if (b32 > b) b = b32;
-  }
-  return b;
 }
 
 template <int D>
@@ -542,10 +518,9 @@ hipError_t launch_prefill(const float* q, const float* kcache, const float* vcac
   a.vcache = vcache;
   a.o = o;
   if (p.partial_slots > 0) {
-    const uint64_t rows = p.x32 ? p.rows_per_tile : kRows;
     char* w = static_cast<char*>(ws);
     a.part_ml = reinterpret_cast<float2*>(w);
-    a.part_acc = reinterpret_cast<float*>(w + ws_align(p.partial_slots * rows * sizeof(float2)));
+    a.part_acc = reinterpret_cast<float*>(w + ws_align(p.partial_slots * kRows * sizeof(float2)));
   }
   a.n_heads = n_heads;
   a.n_kv_heads = n_kv_heads;
@@ -558,9 +533,7 @@ hipError_t launch_prefill(const float* q, const float* kcache, const float* vcac
   a.work_per_kvh = p.work_per_kvh;
   a.kt_per_split = p.ktiles_per_split;
   a.max_splits = p.max_splits;
-  a.pieces = p.pieces;
   a.scale_log2e = (float)(1.4426950408889634 / sqrt((double)head_dim));
-  if (p.x32) return launch_prefill32(a, p, st);
   if (head_dim == 128) return launch_prefill_d<128>(a, p, st);
   return launch_prefill_d<64>(a, p, st);
 }

@@ -1,6 +1,4 @@
-// Shared pieces of the two prefill kernels (prefill.hip: 64-row q tiles on
-// v_mfma_f32_16x16x4f32; prefill32.hip: 128-row q tiles on
-// v_mfma_f32_32x32x2f32): arguments, key-tile counts, and the staging of one
+// Prefill kernel pieces: arguments, key-tile counts, and the staging of one
 // 64-key K/V tile through registers into LDS.
 #pragma once
 
@@ -36,7 +34,6 @@ struct PrefillArgs {
   uint32_t q_per_tile, n_qtiles;
   uint32_t paired, work_per_kvh;
   uint32_t kt_per_split, max_splits;
-  uint32_t pieces;    // 128-row kernel: pieces per q-tile pair
   float scale_log2e;  // fr(1/sqrt(d) * log2(e)): scores in base-2 units
 };
 
@@ -118,15 +115,5 @@ __device__ __forceinline__ void store_tile(const float4 (&pk)[NPF], const float4
   store_k<D, PERM>(pk, k_lds, tid);
   store_v<D>(pv, v_lds, tid);
 }
-
-// The 128-row kernel (prefill32.hip): whether a call takes it, its plan, the
-// partial slots any call within the bounds can need, and its launch.
-bool prefill32_fits(uint32_t n_heads, uint32_t n_kv_heads, uint32_t head_dim,
-                    uint32_t n_queries);
-PrefillPlan prefill32_plan(uint32_t n_heads, uint32_t n_kv_heads, uint32_t n_queries,
-                           uint32_t pos0);
-uint64_t prefill32_slots_bound(uint32_t n_heads, uint32_t n_kv_heads, uint32_t max_queries,
-                               uint32_t max_keys);
-hipError_t launch_prefill32(const PrefillArgs& a, const PrefillPlan& p, hipStream_t st);
 
 }  // namespace flk

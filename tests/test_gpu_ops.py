@@ -423,10 +423,10 @@ def test_prefill_causality_bit_identical(rng):
     assert np.sum(base[5:] != pert[5:]) > H * d
 
 
-# The same two properties on the 128-row kernel (head_dim 128, more than 64
-# query rows), unsplit and with a q tile cut into pieces over a long cache.
+# Causality on longer calls: several q tiles, and a chunk whose keys are
+# split over workgroups and merged (a long cache).
 @pytest.mark.parametrize("nq,pos0,at", [(200, 0, 150), (64, 5000, 30), (300, 40, 7)])
-def test_prefill32_causality_bit_identical(rng, nq, pos0, at):
+def test_prefill_causality_bit_identical_long(rng, nq, pos0, at):
     H, Hkv, d = 16, 8, 128
     nk = pos0 + nq
     q = rand_unit(rng, nq * H * d)
@@ -442,8 +442,8 @@ def test_prefill32_causality_bit_identical(rng, nq, pos0, at):
     assert np.sum(base[at:] != pert[at:]) > H * d
 
 
-def test_prefill32_queries_match_decode(rng):
-    # test_head.ts:321-351 on the 128-row kernel: query `at` equals the decode
+def test_prefill_queries_match_decode_across_tiles(rng):
+    # test_head.ts:321-351 over several q tiles: query `at` equals the decode
     # reference over keys 0 .. at.
     H, Hkv, d, nq = 16, 8, 128, 193
     q = rand_unit(rng, nq * H * d)
