@@ -396,6 +396,28 @@ class Prefill2k(Workload):
         self.work_per_step = layers * self.work_per_call
         self.calls_per_step = layers
 
+    def prologue_line(self, torch, stream, reps=200):
+        """The step's other kernel, timed on its own the same way as the
+        dominant call: R back-to-back flk_qk_prologue calls between events.
+        Its bytes: raw q, k, v read, qn and the k, v cache rows written."""
+        torch.cuda.synchronize()
+        start = torch.cuda.Event(enable_timing=True)
+        end = torch.cuda.Event(enable_timing=True)
+        start.record(stream)
+        for i in range(reps):
+            self.prologue(i % self.L)
+        end.record(stream)
+        torch.cuda.synchronize()
+        us = start.elapsed_time(end) * 1e3 / reps
+        b = 2 * self.n * (H + 2 * HKV) * D * 4
+        gbs = b / (us * 1e-6) / 1e9
+        return {"prologue": {"kernel": "flk_qk_prologue: qk_prologue_kernel<128> (one workgroup "
+                                       "per token)", "bound": "hbm", "bytes_per_launch": b,
+                             "avg_launch_us": round(us, 2), "achieved": round(gbs, 2),
+                             "unit": "GB/s", "peak": HBM_PEAK_GBS,
+                             "frac": round(gbs / HBM_PEAK_GBS, 4),
+                             "share_of_step": round(us * self.L / 1e3 / self.step_ms, 4)}}
+
     def prologue(self, l):
         self.ops.qk_prologue(self.q[l], self.k[l], self.v[l], self.gq[l], self.gk[l], self.inv,
                              EPS, "neox", self.qn[l], self.kc[l], self.vc[l], self.n, self.pos0,
@@ -1144,6 +1166,9 @@ def run(torch, ops, stream, name, steps, warmup):
            "roofline": w.roofline(call_ms, traffic_from_profiles(f"{name}_pmc.md"))}
     if hasattr(w, "extra"):
         out.update(w.extra(ms, call_ms))
+    if hasattr(w, "prologue_line"):
+        w.step_ms = ms
+        out.update(w.prologue_line(torch, stream))
     w.capture()  # host copies of the timed inputs and outputs for the CPU leg
     # Drop the device buffers; the CPU leg needs only the host copies.
     if getattr(w, "graph", None) is not None:

@@ -14,8 +14,14 @@
 
 namespace flk {
 
+// The error text and the current stream belong to the calling host thread:
+// two threads can drive two streams without one's flk_set_stream retargeting
+// the other's launches. g_left_streams: this thread switched away from a
+// non-null stream, which may still hold work that reads buffers (flk_free
+// then waits for the whole device).
 static thread_local char g_err[512] = "";
-static hipStream_t g_stream = nullptr;
+static thread_local hipStream_t g_stream = nullptr;
+static thread_local bool g_left_streams = false;
 
 hipStream_t Stream::get() { return g_stream; }
 
@@ -92,7 +98,9 @@ int32_t flk_device_count(int32_t* count) {
 }
 
 int32_t flk_set_stream(void* stream) {
-  g_stream = static_cast<hipStream_t>(stream);
+  hipStream_t s = static_cast<hipStream_t>(stream);
+  if (g_stream != nullptr && g_stream != s) g_left_streams = true;
+  g_stream = s;
   return FLK_OK;
 }
 
@@ -112,9 +120,15 @@ int32_t flk_free(void* dptr) {
       return fail(FLK_ERR_ARG, "flk_free while the library stream is capturing a graph");
   }
   // Work queued on the library stream may still read this buffer (a caller
-  // can drop its last reference right after a launch): wait for that stream.
-  // hipFree then waits for the rest of the device by itself.
+  // can drop its last reference right after a launch): wait for that stream,
+  // and for the whole device when this thread has launched on other streams
+  // since (streams from flk_stream_create do not synchronise with the null
+  // stream, so the null stream's wait alone would not cover them).
   hipError_t e = hipStreamSynchronize(g_stream);
+  if (e == hipSuccess && g_left_streams) {
+    e = hipDeviceSynchronize();
+    if (e == hipSuccess) g_left_streams = false;
+  }
   if (e == hipSuccess) e = hipFree(dptr);
   return hip_status(e, "hipFree");
 }

@@ -75,6 +75,9 @@ template <int NB, bool FUSE>
 constexpr int q8_unroll() {
   return NB == 1 ? (FUSE ? FLK_Q8_UNROLL_FUSED : FLK_Q8_UNROLL) : (NB == 2 ? 2 : 1);
 }
+#ifndef FLK_Q8_1K
+#define FLK_Q8_1K 1  // rows of 1024 columns take q8_matvec1k_kernel (contiguous row reads)
+#endif
 constexpr int kQ8MaxRegBlocks = 4;  // x blocks per lane kept in registers (8192 columns)
 #ifndef FLK_Q8_LDS_TREE_ROWS
 #define FLK_Q8_LDS_TREE_ROWS 65536
@@ -391,6 +394,175 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
       if (ll == 0 && g0 + waves * u < n_groups && row < a.n_rows) {
         const size_t oi = (size_t)tok * a.n_rows + row;
         if (a.res != nullptr) part = (FLK_Q8_RES_EARLY ? rv[u] : a.res[oi]) + part;
+        if (a.o != nullptr) a.o[oi] = part;
+        if (argmax_better(part, row, bv, bi)) {
+          bv = part;
+          bi = row;
+        }
+      }
+    }
+  }
+  if (a.best_val != nullptr) argmax_block_store(bv, bi, a.best_val, a.best_idx);
+}
+
+// Rows of exactly 1024 columns (32 blocks; the LM head and most of a layer's
+// projections), read contiguously. The kernel above gives lane l block l of a
+// row, so each of its two 16-byte loads per block touches every cache line of
+// the row at half density (a read probe of that pattern over the LM head's
+// bytes: 4.1 TB/s, against 6.0 TB/s when each instruction covers 1 KB
+// contiguously). Here a wave takes rows 2g and 2g + 1 whole: lane L loads
+// bytes 16 L .. 16 L + 15 of each, i.e. half h = L & 1 of block b = L >> 1.
+// The coop(64) order is kept: block b's partial runs through its four word
+// pairs in order -- pairs 0, 1 in the even lane, then, handed over by one DPP
+// move, pairs 2, 3 in the odd lane -- and the blocks' partials (in the odd
+// lanes) meet in the same pairwise tree, logical lane stride m being
+// physical lane stride 2m.
+__device__ __forceinline__ float q8_even_to_odd(float v) {
+  return dpp<0xA0>(v);  // quad_perm [0, 0, 2, 2]: lane 2k + 1 <- lane 2k
+}
+
+// The tree over the odd lanes' 32 block partials (logical strides 16 .. 1 =
+// physical xor 32 .. 2; strides 32 .. 63 of the reference's 64 lanes add
+// exact zeros and are skipped, as in lane_tree).
+template <bool LDS_TREE>
+__device__ __forceinline__ float q8_tree_odd(float v) {
+  if (LDS_TREE) {
+#pragma unroll
+    for (int m = 32; m >= 2; m >>= 1) v = v + shfl_xor(v, m);
+    return v;
+  }
+  v = sum_xor<32>(v);
+  v = sum_xor<16>(v);
+  v = v + xor_lane<8>(v);
+  v = v + dpp<kDppRor4>(v);  // lanes j and j ^ 8 agree: row_ror:4 serves as xor 4
+  v = v + xor_lane<2>(v);
+  return v;
+}
+
+// One row's half block in this lane: words w (quants 16h .. 16h + 15 of block
+// b), x its 16 inputs; returns the block's coop(64) partial in the odd lane.
+__device__ __forceinline__ float q8_half_pair(uint4 w, float scale, const float* x) {
+  const float c0 = q8_dot4(w.x, x) + q8_dot4(w.y, x + 4);
+  const float c1 = q8_dot4(w.z, x + 8) + q8_dot4(w.w, x + 12);
+  const float pe = __builtin_fmaf(scale, c1, __builtin_fmaf(scale, c0, 0.f));  // even: pairs 0, 1
+  const float pin = q8_even_to_odd(pe);
+  return __builtin_fmaf(scale, c1, __builtin_fmaf(scale, c0, pin));  // odd: pairs 2, 3
+}
+
+// Row pairs in flight per wave. 151936 x 1024 (the LM head): 30.8 us with 1,
+// 32.2 with 2, 34.1 with 4, 40.0 with 8 (the kernel above: 31.2 with 2).
+#ifndef FLK_Q8_1K_UNROLL
+#define FLK_Q8_1K_UNROLL 1
+#endif
+#ifndef FLK_Q8_1K_UNROLL_FUSED
+#define FLK_Q8_1K_UNROLL_FUSED 2
+#endif
+template <bool FUSE>
+constexpr int q8_unroll_1k() {
+  return FUSE ? FLK_Q8_1K_UNROLL_FUSED : FLK_Q8_1K_UNROLL;
+}
+
+template <bool FUSE, bool LDS_TREE>
+__global__ __launch_bounds__(kQ8Threads) void q8_matvec1k_kernel(Q8Args a) {
+  constexpr int UR = q8_unroll_1k<FUSE>();
+  constexpr uint32_t kNb = 32;  // blocks per row
+  const int lane = threadIdx.x & 63;
+  const int b = lane >> 1, h = lane & 1;
+  const uint32_t tok = blockIdx.y;
+  const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
+  const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
+  const size_t tok_off = (size_t)tok * a.n_cols;
+  const float* xt = a.x + tok_off;
+  auto ldx = [xt](uint32_t i) { return xt[i]; };
+
+  float nv[kQ8NormBatch];
+  if (FUSE && FLK_Q8_NORM_FIRST) q8_rms_load(lane, a.n_cols, ldx, nv);
+  // Weights, scales and residuals of UR row pairs (rows past the end re-read
+  // the last row, so every load is unconditional).
+  uint4 wa[UR], wb[UR];
+  uint16_t sa[UR], sb[UR];
+  float ra[UR] = {}, rb[UR] = {};
+  auto load = [&](uint32_t g0) {
+#pragma unroll
+    for (int u = 0; u < UR; u++) {
+      const uint32_t r0 = min(2 * (g0 + waves * u), a.n_rows - 1);
+      const uint32_t r1 = min(2 * (g0 + waves * u) + 1, a.n_rows - 1);
+      wa[u] = reinterpret_cast<const uint4*>(a.qs + (size_t)r0 * 1024)[lane];
+      wb[u] = reinterpret_cast<const uint4*>(a.qs + (size_t)r1 * 1024)[lane];
+      sa[u] = a.scales[(size_t)r0 * kNb + b];
+      sb[u] = a.scales[(size_t)r1 * kNb + b];
+      if (FLK_Q8_RES_EARLY && a.res != nullptr) {  // uniform
+        ra[u] = a.res[(size_t)tok * a.n_rows + r0];
+        rb[u] = a.res[(size_t)tok * a.n_rows + r1];
+      }
+    }
+  };
+  load(wave);
+
+  // This lane's 16 inputs: columns 32 b + 16 h .. + 15, after the fusion.
+  float scale = 1.f;
+  if (FUSE && FLK_Q8_NORM_FIRST) {
+    if (a.norm_gain != nullptr) {  // uniform
+      float p0 = 0.f, p1 = 0.f;
+      q8_rms_fold(nv, p0, p1);
+      scale = q8_rms_rest(p0, p1, a.n_cols, a.norm_eps, ldx);
+    }
+  } else if (FUSE) {
+    scale = q8_norm_scale(a, xt);
+  }
+  const uint32_t c0 = 32 * b + 16 * h;
+  float xr[16];
+  {
+    float4 xv[4], yv[4];
+    const float4* xs = reinterpret_cast<const float4*>(xt + c0);
+#pragma unroll
+    for (int i = 0; i < 4; i++) xv[i] = xs[i];
+    if (FUSE) {
+      const float4* ys = reinterpret_cast<const float4*>(
+          a.norm_gain != nullptr ? a.norm_gain + c0 : a.up + tok_off + c0);
+#pragma unroll
+      for (int i = 0; i < 4; i++) yv[i] = ys[i];
+    }
+#pragma unroll
+    for (int i = 0; i < 4; i++) {
+      const float e[4] = {xv[i].x, xv[i].y, xv[i].z, xv[i].w};
+#pragma unroll
+      for (int k = 0; k < 4; k++) {
+        float v = e[k];
+        if (FUSE) {
+          const float y[4] = {yv[i].x, yv[i].y, yv[i].z, yv[i].w};
+          v = a.norm_gain != nullptr ? (v * scale) * y[k] : q8_swiglu(v, y[k]);
+        }
+        xr[4 * i + k] = v;
+      }
+    }
+  }
+
+  float bv = kArgmaxNoVal;
+  uint32_t bi = kArgmaxNoIdx;
+  const uint32_t n_groups = (a.n_rows + 1) / 2;
+  for (uint32_t g0 = wave; g0 < n_groups; g0 += waves * UR) {
+    if (g0 != wave) load(g0);
+#pragma unroll
+    for (int u = 0; u < UR; u++) {
+      float pa = q8_half_pair(wa[u], q8_scale(sa[u]), xr);
+      float pb = q8_half_pair(wb[u], q8_scale(sb[u]), xr);
+      pa = q8_tree_odd<LDS_TREE>(pa);
+      pb = q8_tree_odd<LDS_TREE>(pb);
+      const uint32_t g = g0 + waves * u;
+      const uint32_t r0 = 2 * g;
+      if (lane != 1 || g >= n_groups) continue;
+      if (a.act != nullptr) {  // (gate, up) row pairs -> SwiGLU
+        if (r0 + 1 < a.n_rows) a.act[(size_t)tok * (a.n_rows / 2) + g] = q8_swiglu(pa, pb);
+        continue;
+      }
+#pragma unroll
+      for (int k = 0; k < 2; k++) {
+        const uint32_t row = r0 + k;
+        if (row >= a.n_rows) break;
+        float part = k == 0 ? pa : pb;
+        const size_t oi = (size_t)tok * a.n_rows + row;
+        if (a.res != nullptr) part = (FLK_Q8_RES_EARLY ? (k == 0 ? ra[u] : rb[u]) : a.res[oi]) + part;
         if (a.o != nullptr) a.o[oi] = part;
         if (argmax_better(part, row, bv, bi)) {
           bv = part;
@@ -801,16 +973,21 @@ __global__ __launch_bounds__(kQ8Threads, FLK_Q8_MM_WAVES) void q8_mm_kernel(Q8Ar
 // Workgroups: one resident wave of them (every CU filled to its occupancy
 // limit, so no workgroup waits for another to finish), never more than there
 // are row groups.
-template <int P, int NB, bool FUSE, bool LDS_TREE = false>
+template <int P, int NB, bool FUSE, bool LDS_TREE = false, bool K1 = false>
 static uint32_t q8_grid_x(uint32_t n_groups) {
   static int per_cu = 0;
   if (per_cu == 0) {
     int n = 0;
-    if (FLK_Q8_WG_PER_CU > 0 ||
-        hipOccupancyMaxActiveBlocksPerMultiprocessor(
-            &n, q8_matvec_kernel<P, NB, FUSE, LDS_TREE>, kQ8Threads, 0) !=
-            hipSuccess ||
-        n < 1)
+    hipError_t e = hipSuccess;
+    if (FLK_Q8_WG_PER_CU == 0) {
+      if (K1)
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(&n, q8_matvec1k_kernel<FUSE, LDS_TREE>,
+                                                         kQ8Threads, 0);
+      else
+        e = hipOccupancyMaxActiveBlocksPerMultiprocessor(
+            &n, q8_matvec_kernel<P, NB, FUSE, LDS_TREE>, kQ8Threads, 0);
+    }
+    if (FLK_Q8_WG_PER_CU > 0 || e != hipSuccess || n < 1)
       n = FLK_Q8_WG_PER_CU > 0 ? FLK_Q8_WG_PER_CU : 2;
     per_cu = n;
   }
@@ -822,7 +999,8 @@ static uint32_t q8_grid_x(uint32_t n_groups) {
       cus_of[dev] = 256;
     cus = cus_of[dev];
   }
-  const uint32_t per_wg = (kQ8Threads / kWave) * q8_unroll<NB, FUSE>();
+  const uint32_t per_wg =
+      (kQ8Threads / kWave) * (K1 ? q8_unroll_1k<FUSE>() : q8_unroll<NB, FUSE>());
   const uint32_t need = (n_groups + per_wg - 1) / per_wg;
   const uint32_t cap = (uint32_t)(per_cu * cus);
   return need < cap ? (need > 0 ? need : 1) : cap;
@@ -849,6 +1027,20 @@ static uint32_t launch_q8(const Q8Args& a, hipStream_t st) {
   return gx;
 }
 
+// Rows of 1024 columns: q8_matvec1k_kernel (same grid rule, two rows per wave).
+static uint32_t launch_q8_1k(const Q8Args& a, hipStream_t st) {
+  const uint32_t groups = (a.n_rows + 1) / 2;
+  auto go = [&](auto kernel, uint32_t gx) {
+    hipLaunchKernelGGL(kernel, dim3(gx, a.n_tokens), dim3(kQ8Threads), 0, st, a);
+    return gx;
+  };
+  if (a.norm_gain != nullptr || a.up != nullptr)
+    return go(q8_matvec1k_kernel<true, false>, q8_grid_x<32, 1, true, false, true>(groups));
+  if (a.n_rows >= kQ8LdsTreeRows)
+    return go(q8_matvec1k_kernel<false, true>, q8_grid_x<32, 1, false, true, true>(groups));
+  return go(q8_matvec1k_kernel<false, false>, q8_grid_x<32, 1, false, false, true>(groups));
+}
+
 // Row groups of the register-x kernel and the workgroups it launches at most
 // (the argmax partials of flk_lm_head need one slot per workgroup).
 uint32_t q8_max_workgroups(uint32_t n_rows, uint32_t n_cols) {
@@ -856,7 +1048,8 @@ uint32_t q8_max_workgroups(uint32_t n_rows, uint32_t n_cols) {
   uint32_t P = 1;
   while (P < nb && P < 64) P <<= 1;
   const uint32_t groups = (n_rows + (kWave / P) - 1) / (kWave / P);
-  const uint32_t ub = nb > 128 ? 1 : (nb > 64 ? 2 : FLK_Q8_UNROLL);
+  uint32_t ub = nb > 128 ? 1 : (nb > 64 ? 2 : FLK_Q8_UNROLL);
+  if (nb == 32 && FLK_Q8_1K && FLK_Q8_1K_UNROLL < (int)ub) ub = FLK_Q8_1K_UNROLL;
   const uint32_t per_wg = (kQ8Threads / kWave) * ub;
   return (groups + per_wg - 1) / per_wg;
 }
@@ -913,6 +1106,8 @@ hipError_t launch_q8_matvec(const uint8_t* qs, const uint16_t* scales, const flo
     gx = launch_q8<64, 2>(a, st);
   } else if (nb > 32) {
     gx = launch_q8<64, 1>(a, st);
+  } else if (nb == 32 && FLK_Q8_1K) {
+    gx = launch_q8_1k(a, st);
   } else if (nb > 16) {
     gx = launch_q8<32, 1>(a, st);
   } else if (nb > 8) {

@@ -20,7 +20,9 @@ export const hip = Deno.dlopen(Deno.env.get("FLOCK_ATTN_LIB") ?? "libflock_attn.
   flk_h2d: { parameters: [P, "buffer", U64, U64], result: I32 },
   flk_d2h: { parameters: ["buffer", P, U64, U64], result: I32 },
   flk_memset: { parameters: [P, I32, U64], result: I32 },
-  flk_sync: { parameters: [], result: I32, nonblocking: true },
+  // Blocking: the library's current stream and its error text belong to the
+  // calling thread, so the wait and its status check stay on this thread.
+  flk_sync: { parameters: [], result: I32 },
   flk_workspace_bytes: { parameters: [U32, U32, U32, U32, U32, U32], result: U64 },
   flk_call_workspace_bytes: { parameters: [I32, U32, U32, U32, U32, U32, U32], result: U64 },
   flk_rmsnorm: { parameters: [P, P, P, U32, U32, F32], result: I32 },
@@ -138,9 +140,10 @@ export function download(src: DevPtr, count: number, srcOffset = 0): Float32Arra
   return out;
 }
 
-/** Wait for the library's stream (the mapAsync fence of layer.ts:801-816). */
+/** Wait for the library's stream (the mapAsync fence of layer.ts:801-816);
+ *  a device error surfaces here as a FlockAttnError. Async like mapAsync. */
 export async function sync(): Promise<void> {
-  check(await hip.symbols.flk_sync(), "flk_sync");
+  check(hip.symbols.flk_sync(), "flk_sync");
 }
 
 /** inv_freq[j] = fround(1 / base^(2j/d)), computed on the host as layer.ts:180-186 does. */

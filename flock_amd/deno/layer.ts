@@ -27,6 +27,7 @@ import {
   hip,
   invFreqOf,
   type DevPtr,
+  sync,
   upload,
 } from "./hip_attn.ts";
 
@@ -175,7 +176,7 @@ export class Layer {
 
   /** The attention output of the last encode / encodePrefill. */
   async readOutput(nTokens = 1): Promise<Float32Array> {
-    await hip.symbols.flk_sync();
+    await sync();
     return download(this.buf.attn, nTokens * this.cfg.nHeads * this.cfg.headDim);
   }
 

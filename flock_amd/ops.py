@@ -32,21 +32,34 @@ def _pairing(p) -> int:
 _pending_free: list[int] = []
 
 
-def release_pending() -> None:
-    """Free the buffers collected since the last sync() (waits for the device)."""
+def release_pending(raise_errors: bool = True) -> None:
+    """Free the buffers collected since the last sync() (waits for the device).
+
+    A pointer leaves the list only once flk_free has released it: a refused
+    free (e.g. during a graph capture) keeps it for a later call."""
     while _pending_free:
-        check(lib().flk_free(_pending_free.pop()), "flk_free")
+        rc = lib().flk_free(_pending_free[-1])
+        if rc != 0:
+            if raise_errors:
+                check(rc, "flk_free")
+            return
+        _pending_free.pop()
 
 
 class DeviceBuffer:
     """Device memory from flk_alloc (the reference's storageBuffer).
 
     free() releases it at once (flk_free waits for the device); a buffer that
-    is simply dropped is released at the next sync() / release_pending()."""
+    is simply dropped is released at the next sync(), release_pending() or
+    allocation."""
 
     def __init__(self, nbytes: int):
         if nbytes <= 0:
             raise ValueError("DeviceBuffer needs a positive size")
+        # An allocation is a natural point to return collected buffers (a
+        # loop that only reads results back never calls sync()); a refused
+        # free, as under graph capture, leaves them for later.
+        release_pending(raise_errors=False)
         p = ctypes.c_void_p()
         check(lib().flk_alloc(ctypes.byref(p), nbytes), "flk_alloc")
         self.ptr = p.value

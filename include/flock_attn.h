@@ -25,6 +25,8 @@
  *     message for the calling thread's most recent failure. Nothing throws.
  *   - Launches are asynchronous and ordered on the library's current stream
  *     (flk_set_stream; default: the null stream). flk_sync() waits for it.
+ *     The current stream, like the flk_last_error text, belongs to the
+ *     calling host thread.
  *   - Split-K kernels need scratch for per-split partial results. The caller
  *     passes it as (ws, ws_bytes), sized with flk_workspace_bytes; it needs no
  *     initialisation and holds nothing between calls. Calls that share one
@@ -65,15 +67,17 @@ const char* flk_last_error(void);
 const char* flk_version(void);
 /* Number of visible devices (0 when no GPU); never fails. */
 int32_t flk_device_count(int32_t* count);
-/* Stream for all later launches from this process (hipStream_t; NULL = default).
- * Replaces the caller-supplied GPUCommandEncoder of Layer.encode (layer.ts:586-589). */
+/* Stream for all later launches from the calling thread (hipStream_t; NULL =
+ * default; each host thread starts on NULL). Replaces the caller-supplied
+ * GPUCommandEncoder of Layer.encode (layer.ts:586-589). */
 int32_t flk_set_stream(void* stream);
 
 /* Device memory (storageBuffer / createBuffer, lib.ts:548-566; readBack,
  * lib.ts:575-593). flk_h2d/flk_d2h are synchronous with respect to the host.
- * flk_free waits for the library stream, then releases the memory with
- * hipFree, which waits for the rest of the device: call it outside loops that
- * must not stall. While the library stream is capturing a graph it returns
+ * flk_free waits for the calling thread's library stream -- for the whole
+ * device when that thread has switched away from a non-null stream since its
+ * last such wait -- then releases the memory with hipFree: call it outside
+ * loops that must not stall. While the library stream is capturing a graph it returns
  * FLK_ERR_ARG and frees nothing (free after flk_capture_end). */
 int32_t flk_alloc(void** dptr, uint64_t bytes);
 int32_t flk_free(void* dptr);
