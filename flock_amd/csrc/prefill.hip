@@ -27,12 +27,14 @@
 // of the summed index is the same dot product), so each lane reads D/4
 // contiguous floats of a K row from LDS.
 //
-// Each tile's K/V rows are loaded into registers while the previous tile is
-// computed, then written to LDS. The loads go through a buffer descriptor
-// made per tile (scalar registers): a thread's offset within the tile is the
-// same for every tile, so the fetch costs no per-tile address arithmetic, and
-// rows past the last key read as 0. Causal bound: query at absolute position p
-// sees keys 0..p (attention_prefill.wgsl:90), applied per element.
+// Each tile's K/V rows go from HBM straight into LDS (buffer_load_dwordx4
+// ... lds) while the previous tile is computed: no registers, no LDS store
+// instructions, and one wait + barrier per tile. The loads go through a
+// buffer descriptor made per tile (scalar registers): a lane's offsets within
+// the tile are the same for every tile, so the fetch costs no per-tile
+// address arithmetic, and rows past the last key arrive as 0. Causal bound:
+// query at absolute position p sees keys 0..p (attention_prefill.wgsl:90),
+// applied per element.
 //
 // Scheduling (1-D grid, workgroup id = kv head + n_kv_heads * work item, so
 // with 8 kv heads the workgroups of one kv head share an XCD and its L2):
@@ -41,14 +43,11 @@
 //   split:  too few q tiles to fill the GPU (chunked prefill onto a long
 //           cache): work item (q tile, split) runs a range of key tiles and
 //           writes an (m, l, acc) partial that prefill_merge_kernel combines.
+#include <type_traits>
+
 #include "prefill.hpp"
 
 namespace flk {
-
-#ifndef FLK_PREFILL_KPERM
-#define FLK_PREFILL_KPERM 1  // K rows stored with chunks 8..15 and 16..23 swapped (D = 128)
-#endif
-constexpr bool kKPerm = FLK_PREFILL_KPERM != 0;
 
 // This lane's row of q tile qt in the B-operand layout of S^T = K Q^T (D/4
 // floats from dim (D/4) * lg), pre-multiplied by scale * log2(e) so that S^T
@@ -77,16 +76,18 @@ __device__ __forceinline__ void load_q(float (&qreg)[D / 4], const PrefillArgs& 
 }
 
 // Runs key tiles [kt0, kt1) for q tile qt of kv head kvh; writes o rows
-// (normalised) when `final`, else the partial of `slot`. qreg, pk and pv are
-// the caller's so that one q tile can prefetch for the next: with nxt_qt >= 0
-// the first key tile of q tile nxt_qt (key tile 0) is requested into pk/pv
-// during the last key tile, and its q rows into qreg after the loop (their
-// latency then overlaps the combine); the next call passes preloaded = true.
-template <int D, int NPF = kBK * D / 4 / kPThreads>
-__device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, float* v_lds,
+// (normalised) when `final`, else the partial of `slot`. Tile kt0 is (or, with
+// preloaded, already was) requested into LDS buffer pair p0. qreg is the
+// caller's so that one q tile can prefetch for the next: with nxt_qt >= 0 the
+// first key tile of q tile nxt_qt (key tile 0) is requested into the free
+// buffer pair at the start of the last key tile, and its q rows into qreg
+// after the loop (their latency then overlaps the combine); the next call
+// passes preloaded = true and that pair as its p0.
+template <int D>
+__device__ __forceinline__ void run_qtile(const PrefillArgs& a, const TileBuffers& lb,
                                           uint32_t kvh, uint32_t qt, uint32_t kt0, uint32_t kt1,
                                           bool final, size_t slot, float (&qreg)[D / 4],
-                                          float4 (&pk)[NPF], float4 (&pv)[NPF], bool preloaded,
+                                          const TileOffsets<D>& toff, uint32_t p0, bool preloaded,
                                           int nxt_qt) {
   constexpr int LDK = D + 4;        // padded K row in LDS (floats)
   constexpr int DS = D / 4;         // k-steps of 4 dims for S
@@ -96,6 +97,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   const int lane = tid & 63;
   const int wave = tid >> 6;
   const int half = wave >> 2;  // which 32 keys of every tile this wave takes
+  const int wave_u = __builtin_amdgcn_readfirstlane(wave);
   const int lc = lane & 15;    // column within the 16-block = row of this lane
   const int lg = lane >> 4;    // lane group 0..3
   // V-read swizzle (D = 128): A-operand lane lc supplies channel 8*lc + (c ^
@@ -117,8 +119,10 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   const bool row_ok = r < a.q_per_tile * a.group && qi < a.n_queries;
   const uint32_t qpos = a.pos0 + qi;
 
+  auto k_buf = [&](int b) { return b ? lb.k1 : lb.k0; };
+  auto v_buf = [&](int b) { return b ? lb.v1 : lb.v0; };
   if (!preloaded) {
-    load_tile<D>(pk, pv, a, kvh, kt0, n_keys_total, tid);
+    request_tile<D>(a, k_buf(p0), v_buf(p0), kvh, kt0, n_keys_total, toff, wave_u);
     load_q<D>(qreg, a, kvh, qt);
   }
   floatx4 oacc[CB];
@@ -134,13 +138,8 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   const bool all_rows = a.q_per_tile * a.group == kRows && q0 + a.q_per_tile <= a.n_queries;
   auto full_tile = [&](uint32_t key0) { return all_rows && key0 + kBK - 1 <= a.pos0 + q0; };
 
-  // Two LDS buffers: tile kt is computed from buffer (kt - kt0) & 1 while
-  // tile kt + 1 is stored into the other one and tile kt + 2 loads into
-  // registers; one barrier per tile separates the two.
-  __syncthreads();  // LDS may still hold the previous q tile's merge data
-  store_tile<D, kKPerm>(pk, pv, k_lds, v_lds, tid);
-  load_tile<D>(pk, pv, a, kvh, kt0 + 1 < kt1 ? kt0 + 1 : kt0, n_keys_total, tid);
-  __syncthreads();
+  // Two LDS buffers: tile kt is computed from buffer (p0 + kt - kt0) & 1
+  // while tile kt + 1 loads into the other one; one wait + barrier per tile.
 
   // Operands are read from LDS kAhead groups ahead of the MFMAs that use
   // them; sched_barrier keeps the compiler from sinking each read next to its
@@ -149,9 +148,8 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
   constexpr int NG = DS / 4;        // S: groups of 4 k-steps (one float4 per chain)
   constexpr int NST = kHalfKB * 4;  // PV: k-steps of 4 keys
   // Lane group lg reads chunks 8 lg .. 8 lg + 7 (D = 128) of its key rows.
-  const float* kr0 =
-      &k_lds[((half * kHalfKB) * 16 + lc) * LDK + 4 * k_chunk_pos<D, kKPerm>((DS / 4) * lg)];
-  const float* vr0 = &v_lds[((half * kHalfKB) * 16 + 4 * lg) * D + CB * lc];
+  const int kr0 = ((half * kHalfKB) * 16 + lc) * LDK + 4 * k_chunk_pos<D, kKPerm>((DS / 4) * lg);
+  const int vr0 = ((half * kHalfKB) * 16 + 4 * lg) * D + CB * lc;
   auto k_group = [&](const float* kt_lds_base, int g, int b) {
     return *reinterpret_cast<const floatx4*>(kt_lds_base + b * 16 * LDK + 4 * g);
   };
@@ -160,13 +158,26 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
     return *reinterpret_cast<const floatx4*>(vt_lds_base + (b * 16 + i) * D + 4 * (c4 ^ sw_rd));
   };
 
-  for (uint32_t kt = kt0; kt < kt1; kt++) {
+  // The buffer of every tile is a compile-time choice (B), so that the
+  // compiler sees that the operand reads of one buffer do not depend on the
+  // loads in flight into the other and places no wait for them.
+  auto tile = [&](uint32_t kt, auto bc) {
+    constexpr int B = decltype(bc)::value;
+    float* const k_cur = B ? lb.k1 : lb.k0;
+    float* const v_cur = B ? lb.v1 : lb.v0;
+    float* const k_nxt = B ? lb.k0 : lb.k1;
+    float* const v_nxt = B ? lb.v0 : lb.v1;
     const uint32_t key0 = kt * kBK;
-    const int buf = (kt - kt0) & 1;
-    const float* kb = kr0 + buf * (kBK * LDK);
-    const float* vb = vr0 + buf * (kBK * D);
+    wait_vm0();       // this wave's share of tile kt is in LDS
+    __syncthreads();  // every wave's; every wave is done with tile kt - 1's buffer
+    if (kt + 1 < kt1)
+      request_tile<D>(a, k_nxt, v_nxt, kvh, kt + 1, n_keys_total, toff, wave_u);
+    else if (nxt_qt >= 0)  // the next q tile's first key tile
+      request_tile<D>(a, k_nxt, v_nxt, kvh, 0, n_keys_total, toff, wave_u);
+    const float* kb = k_cur + kr0;
+    const float* vb = v_cur + vr0;
 
-    // The first K groups of this tile (stored before the last barrier).
+    // The first K groups of this tile (in LDS since the barrier).
     floatx4 kg[kAhead + 1][kHalfKB];
 #pragma unroll
     for (int g = 0; g < kAhead; g++)
@@ -186,23 +197,6 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
 #pragma unroll
         for (int b = 0; b < kHalfKB; b++) kg[(g + kAhead) % (kAhead + 1)][b] = k_group(kb, g + kAhead, b);
       }
-      __builtin_amdgcn_sched_barrier(0);
-      // The next tile goes from registers into the free buffers in two
-      // halves, K a quarter of the way through S and V three quarters of the
-      // way (the MFMAs queued so far cover the writes); the tile after it is
-      // requested right after each half (the last one is simply loaded again
-      // at the end).
-      if (g == NG / 4 && kt + 1 < kt1) {
-        store_k<D, kKPerm>(pk, k_lds + (buf ^ 1) * (kBK * LDK), tid);
-        load_rows<D>(pk, a.kcache, a, kvh, kt + 2 < kt1 ? kt + 2 : kt + 1, n_keys_total, tid);
-      }
-      if (g == 3 * NG / 4 && kt + 1 < kt1) {
-        store_v<D>(pv, v_lds + (buf ^ 1) * (kBK * D), tid);
-        load_rows<D>(pv, a.vcache, a, kvh, kt + 2 < kt1 ? kt + 2 : kt + 1, n_keys_total, tid);
-      }
-      // During the last tile, the next q tile's first key tile is requested.
-      if (g == NG / 2 && kt + 1 == kt1 && nxt_qt >= 0)
-        load_tile<D>(pk, pv, a, kvh, 0, n_keys_total, tid);
       __builtin_amdgcn_sched_barrier(0);
 #pragma unroll
       for (int j = 0; j < 4; j++)
@@ -281,23 +275,32 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
                                                        sacc[st / 4][st % 4], oacc[c], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
-    __syncthreads();  // tile kt + 1 stored; buffer of tile kt free again
+  };
+  uint32_t kt = kt0;
+  if (p0 != 0 && kt < kt1) tile(kt++, std::integral_constant<int, 1>{});
+  for (; kt + 1 < kt1; kt += 2) {
+    tile(kt, std::integral_constant<int, 0>{});
+    tile(kt + 1, std::integral_constant<int, 1>{});
   }
+  if (kt < kt1) tile(kt, std::integral_constant<int, 0>{});
+  __syncthreads();  // every wave is done with the last tile's buffers
 
   if (nxt_qt >= 0) load_q<D>(qreg, a, kvh, (uint32_t)nxt_qt);  // the next q tile's rows
   l_run = sum_xor<16>(l_run);  // the row's denominator: its four lane groups
   l_run = sum_xor<32>(l_run);
   // ---- combine the two key halves of each row through LDS --------------------
   // Lane holds channels 4*CB*lg + CB*j + c of its row. The upper waves park
-  // their (m, l, acc) in the (now free) K tile buffer; the lower waves fold
-  // them in and write the row.
-  // Every wave has passed the last tile's barrier, so the K buffers are free.
+  // their acc in the last tile's K buffer and (m, l) in its V buffer; the
+  // lower waves fold them in and write the row.
+  // The last tile's buffers are free (the other pair may be receiving the
+  // next q tile's first key tile).
   // o rows padded to D + FLK_PREFILL_OPAD floats: the 16 lanes of a group
   // hold 16 different rows, which then fall in distinct bank groups.
   constexpr int LDO = D + FLK_PREFILL_OPAD;
-  static_assert(2 * kRows + kRows * LDO <= 2 * kBK * LDK, "combine data exceeds the K buffers");
-  float* m_lds = k_lds;              // [kRows] m, then [kRows] l
-  float* o_lds = k_lds + 2 * kRows;  // [kRows][LDO]
+  static_assert(kRows * LDO <= kBK * LDK && 2 * kRows <= kBK * D, "combine data exceeds a buffer");
+  const int buf_last = (p0 + kt1 - 1 - kt0) & 1;
+  float* m_lds = v_buf(buf_last);  // [kRows] m, then [kRows] l
+  float* o_lds = k_buf(buf_last);  // [kRows][LDO]
   if (half == 1) {
     float* dst = o_lds + r * LDO + 4 * CB * lg;
 #pragma unroll
@@ -346,21 +349,24 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, float* k_lds, fl
 
 template <int D>
 __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
-  __shared__ __attribute__((aligned(16))) float k_lds[2 * kBK * (D + 4)];
-  __shared__ __attribute__((aligned(16))) float v_lds[2 * kBK * D];
+  __shared__ __attribute__((aligned(16))) float k_lds0[kBK * (D + 4)];
+  __shared__ __attribute__((aligned(16))) float k_lds1[kBK * (D + 4)];
+  __shared__ __attribute__((aligned(16))) float v_lds0[kBK * D];
+  __shared__ __attribute__((aligned(16))) float v_lds1[kBK * D];
+  const TileBuffers lb{k_lds0, k_lds1, v_lds0, v_lds1};
   const uint32_t kvh = blockIdx.x % a.n_kv_heads;
   const uint32_t w = blockIdx.x / a.n_kv_heads;
-  constexpr int NPF = kBK * D / 4 / kPThreads;
   float qreg[D / 4];
-  float4 pk[NPF], pv[NPF];
+  TileOffsets<D> toff;
+  tile_offsets<D>(toff, a.n_kv_heads * D * 4, threadIdx.x >> 6, threadIdx.x & 63);
   if (a.paired) {
     const uint32_t qt_hi = a.n_qtiles - 1 - w;
-    run_qtile<D>(a, k_lds, v_lds, kvh, qt_hi, 0,
-                 qtile_kt(qt_hi, a.q_per_tile, a.n_queries, a.pos0), true, 0, qreg, pk, pv, false,
+    const uint32_t n_hi = qtile_kt(qt_hi, a.q_per_tile, a.n_queries, a.pos0);
+    run_qtile<D>(a, lb, kvh, qt_hi, 0, n_hi, true, 0, qreg, toff, 0, false,
                  w < qt_hi ? (int)w : -1);
     if (w < qt_hi)
-      run_qtile<D>(a, k_lds, v_lds, kvh, w, 0, qtile_kt(w, a.q_per_tile, a.n_queries, a.pos0),
-                   true, 0, qreg, pk, pv, true, -1);
+      run_qtile<D>(a, lb, kvh, w, 0, qtile_kt(w, a.q_per_tile, a.n_queries, a.pos0),
+                   true, 0, qreg, toff, n_hi & 1, true, -1);
     return;
   }
   const uint32_t qt = a.n_qtiles - 1 - w / a.max_splits;  // heaviest q tile first
@@ -371,7 +377,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
   const uint32_t kt0 = split * n_kt / ns;
   const uint32_t kt1 = (split + 1) * n_kt / ns;
   const size_t slot = ((size_t)qt * a.max_splits + split) * a.n_kv_heads + kvh;
-  run_qtile<D>(a, k_lds, v_lds, kvh, qt, kt0, kt1, ns == 1, slot, qreg, pk, pv, false, -1);
+  run_qtile<D>(a, lb, kvh, qt, kt0, kt1, ns == 1, slot, qreg, toff, 0, false, -1);
 }
 
 // One workgroup per (kv head, q tile, 256 / (D/4) rows); D/4 lanes per row,
