@@ -49,12 +49,11 @@
 
 namespace flk {
 
-// This lane's row of q tile qt in the B-operand layout of S^T = K Q^T (D/4
-// floats from dim (D/4) * lg), pre-multiplied by scale * log2(e) so that S^T
-// comes out in base-2 units.
+// Requests this lane's row of q tile qt in the B-operand layout of S^T = K
+// Q^T: D/4 floats from dim (D/4) * lg.
 template <int D>
-__device__ __forceinline__ void load_q(float (&qreg)[D / 4], const PrefillArgs& a, uint32_t kvh,
-                                       uint32_t qt) {
+__device__ __forceinline__ void fetch_q(float4 (&qraw)[D / 16], const PrefillArgs& a,
+                                        uint32_t kvh, uint32_t qt) {
   constexpr int DS = D / 4;
   const int lane = threadIdx.x & 63, wave = threadIdx.x >> 6;
   const int lc = lane & 15, lg = lane >> 4;
@@ -66,27 +65,35 @@ __device__ __forceinline__ void load_q(float (&qreg)[D / 4], const PrefillArgs& 
   const float4* src = reinterpret_cast<const float4*>(
       a.q + ((size_t)(row_ok ? qi : q0) * a.n_heads + (row_ok ? h : kvh * a.group)) * D + DS * lg);
 #pragma unroll
-  for (int s4 = 0; s4 < DS / 4; s4++) {
-    const float4 v = src[s4];
-    qreg[4 * s4 + 0] = v.x * a.scale_log2e;
-    qreg[4 * s4 + 1] = v.y * a.scale_log2e;
-    qreg[4 * s4 + 2] = v.z * a.scale_log2e;
-    qreg[4 * s4 + 3] = v.w * a.scale_log2e;
+  for (int s4 = 0; s4 < DS / 4; s4++) qraw[s4] = src[s4];
+}
+
+// The fetched row pre-multiplied by scale * log2(e), so that S^T comes out in
+// base-2 units.
+template <int D>
+__device__ __forceinline__ void scale_q(float (&qreg)[D / 4], const float4 (&qraw)[D / 16],
+                                        const PrefillArgs& a) {
+#pragma unroll
+  for (int s4 = 0; s4 < D / 16; s4++) {
+    qreg[4 * s4 + 0] = qraw[s4].x * a.scale_log2e;
+    qreg[4 * s4 + 1] = qraw[s4].y * a.scale_log2e;
+    qreg[4 * s4 + 2] = qraw[s4].z * a.scale_log2e;
+    qreg[4 * s4 + 3] = qraw[s4].w * a.scale_log2e;
   }
 }
 
 // Runs key tiles [kt0, kt1) for q tile qt of kv head kvh; writes o rows
 // (normalised) when `final`, else the partial of `slot`. Tile kt0 is (or, with
-// preloaded, already was) requested into LDS buffer pair p0. qreg is the
-// caller's so that one q tile can prefetch for the next: with nxt_qt >= 0 the
-// first key tile of q tile nxt_qt (key tile 0) is requested into the free
-// buffer pair at the start of the last key tile, and its q rows into qreg
-// after the loop (their latency then overlaps the combine); the next call
-// passes preloaded = true and that pair as its p0.
+// preloaded, already was) requested into LDS buffer pair p0, and this lane's
+// q row into qraw (the caller's). With nxt_qt >= 0, the first key tile of q
+// tile nxt_qt (key tile 0) is requested into the free buffer pair, and its q
+// rows into qraw, at the start of the last key tile, so that their latency
+// overlaps that tile and the combine; the next call passes preloaded = true
+// and that pair as its p0.
 template <int D>
 __device__ __forceinline__ void run_qtile(const PrefillArgs& a, const TileBuffers& lb,
                                           uint32_t kvh, uint32_t qt, uint32_t kt0, uint32_t kt1,
-                                          bool final, size_t slot, float (&qreg)[D / 4],
+                                          bool final, size_t slot, float4 (&qraw)[D / 16],
                                           const TileOffsets<D>& toff, uint32_t p0, bool preloaded,
                                           int nxt_qt) {
   constexpr int LDK = D + 4;        // padded K row in LDS (floats)
@@ -123,8 +130,14 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, const TileBuffer
   auto v_buf = [&](int b) { return b ? lb.v1 : lb.v0; };
   if (!preloaded) {
     request_tile<D>(a, k_buf(p0), v_buf(p0), kvh, kt0, n_keys_total, toff, wave_u);
-    load_q<D>(qreg, a, kvh, qt);
+    fetch_q<D>(qraw, a, kvh, qt);
   }
+  float qreg[D / 4];
+  scale_q<D>(qreg, qraw, a);
+  wait_vm0();       // this wave's share of tile kt0 is in LDS
+  __syncthreads();  // every wave's; the previous q tile's combine is done
+  // The next q tile's rows: in flight during the first key tile, then held.
+  if (nxt_qt >= 0) fetch_q<D>(qraw, a, kvh, (uint32_t)nxt_qt);
   floatx4 oacc[CB];
 #pragma unroll
   for (int c = 0; c < CB; c++) oacc[c] = floatx4{0.f, 0.f, 0.f, 0.f};
@@ -138,8 +151,9 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, const TileBuffer
   const bool all_rows = a.q_per_tile * a.group == kRows && q0 + a.q_per_tile <= a.n_queries;
   auto full_tile = [&](uint32_t key0) { return all_rows && key0 + kBK - 1 <= a.pos0 + q0; };
 
-  // Two LDS buffers: tile kt is computed from buffer (p0 + kt - kt0) & 1
-  // while tile kt + 1 loads into the other one; one wait + barrier per tile.
+  // Two LDS buffer pairs: tile kt is computed from pair (p0 + kt - kt0) & 1
+  // while tile kt + 1 loads into the other one; a wait + barrier ends each
+  // tile.
 
   // Operands are read from LDS kAhead groups ahead of the MFMAs that use
   // them; sched_barrier keeps the compiler from sinking each read next to its
@@ -168,8 +182,6 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, const TileBuffer
     float* const k_nxt = B ? lb.k0 : lb.k1;
     float* const v_nxt = B ? lb.v0 : lb.v1;
     const uint32_t key0 = kt * kBK;
-    wait_vm0();       // this wave's share of tile kt is in LDS
-    __syncthreads();  // every wave's; every wave is done with tile kt - 1's buffer
     if (kt + 1 < kt1)
       request_tile<D>(a, k_nxt, v_nxt, kvh, kt + 1, n_keys_total, toff, wave_u);
     else if (nxt_qt >= 0)  // the next q tile's first key tile
@@ -230,7 +242,7 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, const TileBuffer
 #pragma unroll
         for (int i = 0; i < 4; i++) {
           const uint32_t key = key0 + (half * kHalfKB + b) * 16 + 4 * lg + i;
-          if (!(row_ok && key <= qpos)) sacc[b][i] = -INFINITY;
+          sacc[b][i] = row_ok && key <= qpos ? sacc[b][i] : -INFINITY;
         }
     }
     float lmx = sacc[0][0];
@@ -275,6 +287,8 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, const TileBuffer
                                                        sacc[st / 4][st % 4], oacc[c], 0, 0, 0);
       __builtin_amdgcn_sched_barrier(0);
     }
+    wait_vm0();       // this wave's share of the next tile is in LDS
+    __syncthreads();  // every wave's; every wave is done with this tile's buffers
   };
   uint32_t kt = kt0;
   if (p0 != 0 && kt < kt1) tile(kt++, std::integral_constant<int, 1>{});
@@ -283,17 +297,15 @@ __device__ __forceinline__ void run_qtile(const PrefillArgs& a, const TileBuffer
     tile(kt + 1, std::integral_constant<int, 1>{});
   }
   if (kt < kt1) tile(kt, std::integral_constant<int, 0>{});
-  __syncthreads();  // every wave is done with the last tile's buffers
 
-  if (nxt_qt >= 0) load_q<D>(qreg, a, kvh, (uint32_t)nxt_qt);  // the next q tile's rows
   l_run = sum_xor<16>(l_run);  // the row's denominator: its four lane groups
   l_run = sum_xor<32>(l_run);
   // ---- combine the two key halves of each row through LDS --------------------
   // Lane holds channels 4*CB*lg + CB*j + c of its row. The upper waves park
   // their acc in the last tile's K buffer and (m, l) in its V buffer; the
   // lower waves fold them in and write the row.
-  // The last tile's buffers are free (the other pair may be receiving the
-  // next q tile's first key tile).
+  // The last tile's buffers are free (the other pair may hold the next q
+  // tile's first key tile).
   // o rows padded to D + FLK_PREFILL_OPAD floats: the 16 lanes of a group
   // hold 16 different rows, which then fall in distinct bank groups.
   constexpr int LDO = D + FLK_PREFILL_OPAD;
@@ -356,17 +368,17 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
   const TileBuffers lb{k_lds0, k_lds1, v_lds0, v_lds1};
   const uint32_t kvh = blockIdx.x % a.n_kv_heads;
   const uint32_t w = blockIdx.x / a.n_kv_heads;
-  float qreg[D / 4];
+  float4 qraw[D / 16];
   TileOffsets<D> toff;
   tile_offsets<D>(toff, a.n_kv_heads * D * 4, threadIdx.x >> 6, threadIdx.x & 63);
   if (a.paired) {
     const uint32_t qt_hi = a.n_qtiles - 1 - w;
     const uint32_t n_hi = qtile_kt(qt_hi, a.q_per_tile, a.n_queries, a.pos0);
-    run_qtile<D>(a, lb, kvh, qt_hi, 0, n_hi, true, 0, qreg, toff, 0, false,
+    run_qtile<D>(a, lb, kvh, qt_hi, 0, n_hi, true, 0, qraw, toff, 0, false,
                  w < qt_hi ? (int)w : -1);
     if (w < qt_hi)
       run_qtile<D>(a, lb, kvh, w, 0, qtile_kt(w, a.q_per_tile, a.n_queries, a.pos0),
-                   true, 0, qreg, toff, n_hi & 1, true, -1);
+                   true, 0, qraw, toff, n_hi & 1, true, -1);
     return;
   }
   const uint32_t qt = a.n_qtiles - 1 - w / a.max_splits;  // heaviest q tile first
@@ -377,7 +389,7 @@ __global__ __launch_bounds__(kPThreads) void prefill_kernel(PrefillArgs a) {
   const uint32_t kt0 = split * n_kt / ns;
   const uint32_t kt1 = (split + 1) * n_kt / ns;
   const size_t slot = ((size_t)qt * a.max_splits + split) * a.n_kv_heads + kvh;
-  run_qtile<D>(a, lb, kvh, qt, kt0, kt1, ns == 1, slot, qreg, toff, 0, false, -1);
+  run_qtile<D>(a, lb, kvh, qt, kt0, kt1, ns == 1, slot, qraw, toff, 0, false, -1);
 }
 
 // One workgroup per (kv head, q tile, 256 / (D/4) rows); D/4 lanes per row,
