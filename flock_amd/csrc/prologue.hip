@@ -132,7 +132,10 @@ __global__ __launch_bounds__(kPrologueThreads) void qk_prologue_kernel(
     uint32_t n_kv_heads, uint32_t q_stride, uint32_t kv_stride, RaggedTokens rt) {
   __shared__ float2 s_cs[D / 2];
   const int lane = threadIdx.x & 63;
-  const int wave = threadIdx.x >> 6;
+  // The wave index in a scalar register: the compiler then knows each vector
+  // index is wave-uniform, so locate()'s branches and row addresses are scalar
+  // work instead of exec-masked vector code.
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const uint32_t tok = blockIdx.x;
   uint32_t pos = pos0 + tok;
   uint64_t cache_row = pos;
