@@ -305,7 +305,10 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_kernel(Q8Args a) {
   const uint32_t tok = blockIdx.y;
   const uint32_t nb = a.n_cols / 32;
   const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
-  const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
+  // Read through readfirstlane, the wave index is known to be wave-uniform:
+  // the row loop's control and row addresses are then scalar work.
+  const uint32_t wave =
+      blockIdx.x * (kQ8Threads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
 
   // The first row groups' weights (and residuals) are requested before x is
   // prepared, so the input fusion's latency overlaps their fetch.
@@ -470,7 +473,8 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec1k_kernel(Q8Args a) {
   const int b = lane >> 1, h = lane & 1;
   const uint32_t tok = blockIdx.y;
   const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
-  const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
+  const uint32_t wave =
+      blockIdx.x * (kQ8Threads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const size_t tok_off = (size_t)tok * a.n_cols;
   const float* xt = a.x + tok_off;
   auto ldx = [xt](uint32_t i) { return xt[i]; };
@@ -581,7 +585,8 @@ __global__ __launch_bounds__(kQ8Threads) void q8_matvec_wide_kernel(Q8Args a) {
   const uint32_t tok = blockIdx.y;
   const uint32_t nb = a.n_cols / 32;
   const uint32_t waves = gridDim.x * (kQ8Threads / kWave);
-  const uint32_t wave = blockIdx.x * (kQ8Threads / kWave) + (threadIdx.x >> 6);
+  const uint32_t wave =
+      blockIdx.x * (kQ8Threads / kWave) + __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const size_t tok_off = (size_t)tok * a.n_cols;
   const float* xt = a.x + tok_off;
   const float scale = q8_norm_scale(a, xt);
