@@ -665,7 +665,8 @@ class Q8LmHead(Workload):
             "scales), seeded N(0,1) inputs, zeroed or seeded caches")
 
     name = "q8lmhead"
-    kernel = "flk_q8_matvec: q8_matvec_kernel<32,1> (coop(64) order, 2 rows per wave)"
+    kernel = ("flk_q8_matvec: q8_matvec1k_kernel (coop(64) order, 1024-column rows read "
+              "contiguously)")
     rows, cols, copies = 151936, 1024, 3
 
     def __init__(self, torch, ops):
@@ -802,7 +803,8 @@ class Q8Prefill(Workload):
     name = "q8prefill"
     unit = "TFLOP/s"
     bound = "valu"
-    kernel = "flk_q8_gate_up_swiglu: q8_mm_kernel<true,false> (32 rows x 8 tokens per workgroup)"
+    kernel = ("flk_q8_gate_up_swiglu: q8_mm1_kernel<kMmNorm> (32 rows x 8 tokens per tile, "
+              "8 row tiles per workgroup)")
     n_tokens, ffn, hid = 2048, 3072, 1024
 
     def __init__(self, torch, ops):
@@ -962,8 +964,8 @@ class Token(Workload):
             "scales), seeded N(0,1) inputs, zeroed or seeded caches")
 
     unit = "GB/s"
-    kernel = ("DecoderLayer.encode x 28 + flk_lm_head (q8_matvec_kernel, decode_split/merge, "
-              "argmax_final_kernel)")
+    kernel = ("DecoderLayer.encode x 28 + flk_lm_head (q8_matvec1k_kernel, q8_matvec_kernel, "
+              "decode_split/merge, argmax_final_kernel)")
     n_keys = 32769
     layers = 28
 
