@@ -146,6 +146,31 @@ def test_prefill_2048_tokens(rng):
     assert oracle.abs_err_scaled(got, want, oracle.amax(want)) < 1e-5  # test_head.ts:312-316
 
 
+def test_prefill_8192_tokens_sampled_rows(rng):
+    # A prompt four times the benchmark's (paired schedule, 512 workgroups):
+    # every head of 40 rows -- tile edges, the first and last rows, random
+    # ones -- against the oracle's attention of that query over keys 0..p
+    # (attnRef, ops_ref.ts:135-174) and the float64 closed form.
+    n = 8192
+    q, k, v = randn(rng, n * H * D), randn(rng, n * HKV * D), randn(rng, n * HKV * D)
+    o = ops.DeviceBuffer(n * H * D * 4)
+    ops.attn_prefill(dev(q), dev(k), dev(v), o, H, HKV, D, n, 0, ops.Workspace(H, HKV, D, n, n))
+    ops.sync()
+    got = o.download(n * H * D).reshape(n, H * D)
+    rows = sorted({0, 31, 32, 63, 64, 2047, 2048, 4095, 4096, 8127, 8128, 8191,
+                   *rng.integers(0, n, 28).tolist()})
+    qs = q.reshape(n, H * D)
+    g = np.concatenate([got[p] for p in rows])
+    w = np.concatenate([oracle.attn(qs[p], k[:(p + 1) * HKV * D], v[:(p + 1) * HKV * D], H, HKV,
+                                    D, p + 1) for p in rows])
+    f = np.concatenate([cf.attention(qs[p], k[:(p + 1) * HKV * D], v[:(p + 1) * HKV * D], H, HKV,
+                                     D, 1, p) for p in rows])
+    m = metrics(g, w, f)
+    ids = check_ids("prefill 8192, sampled rows", g, w, len(rows) * H, m["max_abs"])
+    record("prefill, 8192 tokens (40 rows)", m, **ids)
+    assert meets_bar(m), fmt(m)
+
+
 def test_chunk_onto_32k_cache(rng):
     # One layer of a 64-token chunk at position 32768 (split keys +
     # merge), compared on every row.

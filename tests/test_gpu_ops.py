@@ -425,7 +425,8 @@ def test_prefill_causality_bit_identical(rng):
 
 # Causality on longer calls: several q tiles, and a chunk whose keys are
 # split over workgroups and merged (a long cache).
-@pytest.mark.parametrize("nq,pos0,at", [(200, 0, 150), (64, 5000, 30), (300, 40, 7)])
+@pytest.mark.parametrize("nq,pos0,at", [(200, 0, 150), (64, 5000, 30), (300, 40, 7),
+                                         (8192, 0, 5000)])
 def test_prefill_causality_bit_identical_long(rng, nq, pos0, at):
     H, Hkv, d = 16, 8, 128
     nk = pos0 + nq

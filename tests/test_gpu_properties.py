@@ -14,7 +14,8 @@ Two inputs make attention's answer known exactly:
 
 The sizes are the benchmark configurations': decode over 32769 keys, causal
 prefill of 2048 tokens, and a 64-token chunk onto 32768 cached keys (key
-splits + merge); and past them, where the reference stops at its $MAX_KEYS
+splits + merge); a prompt of 8192 tokens (512 paired q-tile workgroups) and
+a 1000-token chunk at 20000 (key splits over 32 q tiles); and past them, where the reference stops at its $MAX_KEYS
 workgroup array and the oracle would take minutes: 131073 keys (1 GiB of
 K/V per layer), decode and a 64-token chunk. There a dropped 4-key block
 moves the mean by ~3e-5; rounding by ~1e-9.
@@ -79,7 +80,8 @@ def test_decode_uniform_v_is_returned(rng, nk):
     assert rel < 1e-5, rel
 
 
-@pytest.mark.parametrize("n,pos0", [(2048, 0), (64, 32768), (64, 131072)])
+@pytest.mark.parametrize("n,pos0", [(2048, 0), (8192, 0), (1000, 20000), (64, 32768),
+                                    (64, 131072)])
 def test_prefill_equal_keys_give_causal_prefix_means(rng, n, pos0):
     nk = pos0 + n
     k, v = equal_keys(rng, nk), randn(rng, nk * HKV * D)
@@ -95,7 +97,8 @@ def test_prefill_equal_keys_give_causal_prefix_means(rng, n, pos0):
     assert err < 2e-7, err
 
 
-@pytest.mark.parametrize("n,pos0", [(2048, 0), (64, 32768), (64, 131072)])
+@pytest.mark.parametrize("n,pos0", [(2048, 0), (8192, 0), (1000, 20000), (64, 32768),
+                                    (64, 131072)])
 def test_prefill_uniform_v_is_returned(rng, n, pos0):
     nk = pos0 + n
     k = randn(rng, nk * HKV * D)
