@@ -171,6 +171,29 @@ def test_prefill_8192_tokens_sampled_rows(rng):
     assert meets_bar(m), fmt(m)
 
 
+@pytest.mark.parametrize("h,hkv,d", [(16, 8, 64), (14, 2, 64)])
+def test_prefill_2048_tokens_head_dim_64_sampled_rows(rng, h, hkv, d):
+    # head_dim 64 through the paired schedule (the second q tile of a
+    # workgroup starts in either LDS buffer pair): every head of 24 rows
+    # against the oracle's single-query attention and the float64 closed form.
+    n = 2048
+    q, k, v = randn(rng, n * h * d), randn(rng, n * hkv * d), randn(rng, n * hkv * d)
+    o = ops.DeviceBuffer(n * h * d * 4)
+    ops.attn_prefill(dev(q), dev(k), dev(v), o, h, hkv, d, n, 0, ops.Workspace(h, hkv, d, n, n))
+    ops.sync()
+    got = o.download(n * h * d).reshape(n, h * d)
+    rows = sorted({0, 31, 32, 63, 64, 1023, 1024, 2047, *rng.integers(0, n, 16).tolist()})
+    qs = q.reshape(n, h * d)
+    g = np.concatenate([got[p] for p in rows])
+    w = np.concatenate([oracle.attn(qs[p], k[:(p + 1) * hkv * d], v[:(p + 1) * hkv * d], h, hkv,
+                                    d, p + 1) for p in rows])
+    f = np.concatenate([cf.attention(qs[p], k[:(p + 1) * hkv * d], v[:(p + 1) * hkv * d], h, hkv,
+                                     d, 1, p) for p in rows])
+    m = metrics(g, w, f)
+    record(f"prefill 2048, H {h} / {hkv}, d {d} ({len(rows)} rows)", m)
+    assert meets_bar(m), fmt(m)
+
+
 def test_chunk_onto_32k_cache(rng):
     # One layer of a 64-token chunk at position 32768 (split keys +
     # merge), compared on every row.
