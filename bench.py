@@ -128,6 +128,7 @@ class Workload:
     bound = "hbm"
     calls_per_step = 1
     graph_step = False  # step() replays a captured graph: call time = step time / calls
+    roofline_note = None
     data = ("synthetic: seeded N(0,1) q/k/v and K/V caches, norm gains N(1,0.1); no weights "
             "(attention path only)")
 
@@ -153,6 +154,8 @@ class Workload:
         if self.bound == "mixed":
             out["note"] = ("flops of fp32-MFMA attention and VALU projections together, against "
                            "the fp32 vector peak")
+        if self.roofline_note:
+            out["note"] = self.roofline_note
         return out
 
     # CPU leg: capture() keeps host copies of the timed inputs and the GPU's
@@ -353,6 +356,8 @@ class Decode512(Decode32k):
     kernel = ("flk_decode_layer x 28 replayed from one HIP graph: decode_split_kernel<128,2,8> + "
               "decode_merge_kernel<128> per call")
     graph_step = True
+    roofline_note = ("latency-bound: a call reads 4.2 MB, which HBM would deliver in ~0.5 us; "
+                     "the two kernels' launch and memory latency set its time")
 
     def __init__(self, torch, ops):
         super().__init__(torch, ops, layers=28, n_keys=513)
